@@ -1,0 +1,335 @@
+// Row-wise kernels of the decode path: embedding gather, residual add + RMSNorm, per-head
+// q/k RMSNorm + RoPE with the K/V cache write, SwiGLU, KV compaction of an accepted tree
+// path, the synthetic-weight generator and the greedy argmax reduction.
+//
+// All of them are HBM/latency bound byte movers: 128-bit loads along a row, one workgroup
+// (or one wave) per row/head, fp32 arithmetic with the reference's bf16 rounding points.
+#include "qd_launch.h"
+
+// ------------------------------------------------------------------ embedding gather
+// x[i, :] = table[ids[i], :] -- a bit copy (F.embedding, engine.py:338; embed_ss fast.py:53-70).
+// An id outside [0, vocab) writes a zero row instead of reading out of bounds (the host
+// rejects such ids before they reach the device).
+__global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ ids,
+                                                    const bf16_t* __restrict__ table,
+                                                    bf16_t* __restrict__ out, int64_t vocab,
+                                                    int64_t hidden, int64_t out_stride) {
+  const int64_t i = blockIdx.x;
+  const int64_t id = ids[i];
+  const bool ok = id >= 0 && id < vocab;
+  const int64_t nch = hidden / 8;
+  const uint4* src = reinterpret_cast<const uint4*>(table + (ok ? id : 0) * hidden);
+  uint4* dst = reinterpret_cast<uint4*>(out + i * out_stride);
+  for (int64_t c = threadIdx.x; c < nch; c += blockDim.x) {
+    uint4 v = ok ? src[c] : make_uint4(0, 0, 0, 0);
+    dst[c] = v;
+  }
+}
+
+void launch_embed(const int64_t* ids, const bf16_t* table, bf16_t* out, int64_t n, int64_t vocab,
+                  int64_t hidden, int64_t out_stride, hipStream_t s) {
+  if (n <= 0) return;
+  embed_kernel<<<dim3((unsigned)n), dim3(256), 0, s>>>(ids, table, out, vocab, hidden, out_stride);
+}
+
+// ------------------------------------------------------------------ residual add + RMSNorm
+// r' = bf16(x + r) (x may be null: r' = r), y = bf16(bf16(r' * rstd) * w),
+// rstd = 1 / sqrt(mean(r'^2) + eps) from the bf16-rounded residual (rmsnorm.py:15-32,
+// TF:modeling_qwen3.py:59-64, 304-322).  One workgroup per row.
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  float t = red[0] + red[1] + red[2] + red[3];
+  __syncthreads();
+  return t;
+}
+
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(
+    const bf16_t* __restrict__ x, const bf16_t* res, const bf16_t* __restrict__ w,
+    bf16_t* res_out, bf16_t* __restrict__ y, int64_t hidden, int64_t in_stride,
+    int64_t y_stride, float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int64_t nch = hidden / 8;
+  const uint4* xr = x ? reinterpret_cast<const uint4*>(x + row * in_stride) : nullptr;
+  const uint4* rr = reinterpret_cast<const uint4*>(res + row * in_stride);
+  uint4* ro = res_out ? reinterpret_cast<uint4*>(res_out + row * in_stride) : nullptr;
+  float ss = 0.f;
+  for (int64_t c = threadIdx.x; c < nch; c += 256) {
+    uint4 r = rr[c];
+    if (xr) {
+      uint4 a = xr[c];
+      r.x = pack2(bflo(a.x) + bflo(r.x), bfhi(a.x) + bfhi(r.x));
+      r.y = pack2(bflo(a.y) + bflo(r.y), bfhi(a.y) + bfhi(r.y));
+      r.z = pack2(bflo(a.z) + bflo(r.z), bfhi(a.z) + bfhi(r.z));
+      r.w = pack2(bflo(a.w) + bflo(r.w), bfhi(a.w) + bfhi(r.w));
+    }
+    ss += bflo(r.x) * bflo(r.x) + bfhi(r.x) * bfhi(r.x) + bflo(r.y) * bflo(r.y) +
+          bfhi(r.y) * bfhi(r.y) + bflo(r.z) * bflo(r.z) + bfhi(r.z) * bfhi(r.z) +
+          bflo(r.w) * bflo(r.w) + bfhi(r.w) * bfhi(r.w);
+  }
+  const float rstd = rstd_of(block_sum256(ss, red), (int)hidden, eps);
+  const uint4* wr = reinterpret_cast<const uint4*>(w);
+  uint4* yr = reinterpret_cast<uint4*>(y + row * y_stride);
+  for (int64_t c = threadIdx.x; c < nch; c += 256) {
+    uint4 r = rr[c];
+    if (xr) {
+      uint4 a = xr[c];
+      r.x = pack2(bflo(a.x) + bflo(r.x), bfhi(a.x) + bfhi(r.x));
+      r.y = pack2(bflo(a.y) + bflo(r.y), bfhi(a.y) + bfhi(r.y));
+      r.z = pack2(bflo(a.z) + bflo(r.z), bfhi(a.z) + bfhi(r.z));
+      r.w = pack2(bflo(a.w) + bflo(r.w), bfhi(a.w) + bfhi(r.w));
+    }
+    const uint4 g = wr[c];
+    uint4 o;
+    o.x = pack2(norm_elem(bflo(r.x), rstd, bflo(g.x)), norm_elem(bfhi(r.x), rstd, bfhi(g.x)));
+    o.y = pack2(norm_elem(bflo(r.y), rstd, bflo(g.y)), norm_elem(bfhi(r.y), rstd, bfhi(g.y)));
+    o.z = pack2(norm_elem(bflo(r.z), rstd, bflo(g.z)), norm_elem(bfhi(r.z), rstd, bfhi(g.z)));
+    o.w = pack2(norm_elem(bflo(r.w), rstd, bflo(g.w)), norm_elem(bfhi(r.w), rstd, bfhi(g.w)));
+    yr[c] = o;
+    // each thread writes back exactly the chunks it read, after its last read of them
+    if (ro && xr) ro[c] = r;
+  }
+}
+
+void launch_add_rmsnorm(const bf16_t* x, const bf16_t* res, const bf16_t* w, bf16_t* res_out,
+                        bf16_t* y, int64_t rows, int64_t hidden, int64_t in_stride,
+                        int64_t y_stride, float eps, hipStream_t s) {
+  if (rows <= 0) return;
+  add_rmsnorm_kernel<<<dim3((unsigned)rows), dim3(256), 0, s>>>(x, res, w, res_out, y, hidden,
+                                                                 in_stride, y_stride, eps);
+}
+
+// ------------------------------------------------------------------ q/k RMSNorm + RoPE + KV write
+// One wave per (token row, head in [0, Hq + 2 Hkv)); lane l owns dims l and l + 64, which are
+// exactly the rotate_half partners.  Per-head RMSNorm (q_norm / k_norm weights), then
+//   o1 = bf16(bf16(y1 c1) + bf16(-y2 s1)),  o2 = bf16(bf16(y2 c2) + bf16(y1 s2))
+// (fused.py:24-81, tree.py:26-69, TF:modeling_qwen3.py:140-170, 252-257).  V heads are
+// copied unnormalised into the cache.  Position of token t of row b:
+//   POS_T t | POS_SHARED pos[0]+t | POS_ROW pos[b]+t | POS_CHUNK pos[b]+t (= slot)
+//   POS_TREE: RoPE at pos[b] + depth[b*T + t], cache slot pos[b] + t.
+__global__ __launch_bounds__(64) void qk_norm_rope_kernel(
+    const bf16_t* __restrict__ qkv, int64_t qkv_stride, const bf16_t* __restrict__ qn,
+    const bf16_t* __restrict__ kn, const bf16_t* __restrict__ cos_t,
+    const bf16_t* __restrict__ sin_t, int64_t table_len, const int64_t* __restrict__ pos,
+    const int64_t* __restrict__ depth, int mode, bf16_t* __restrict__ q_out,
+    bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache, int64_t T, int Hq, int Hkv,
+    int64_t cap, float eps) {
+  const int64_t row = blockIdx.x;
+  const int head = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int64_t b = row / T, t = row % T;
+  int64_t rpos, slot;
+  switch (mode) {
+    case POS_T: rpos = slot = t; break;
+    case POS_SHARED: rpos = slot = pos[0] + t; break;
+    case POS_TREE: slot = pos[b] + t; rpos = pos[b] + depth[row]; break;
+    default: rpos = slot = pos[b] + t; break;  // POS_ROW, POS_CHUNK
+  }
+  const bf16_t* src = qkv + row * qkv_stride + (int64_t)head * 128;
+  if (head >= Hq + Hkv) {  // V: copy into the cache as is
+    if (slot < 0 || slot >= cap) return;
+    const int vh = head - Hq - Hkv;
+    bf16_t* dst = v_cache + ((b * Hkv + vh) * cap + slot) * 128;
+    dst[lane] = src[lane];
+    dst[lane + 64] = src[lane + 64];
+    return;
+  }
+  if (rpos < 0 || rpos >= table_len) return;
+  const float x1 = bf2f(src[lane]), x2 = bf2f(src[lane + 64]);
+  const float r = rstd_of(wave_sum(x1 * x1 + x2 * x2), 128, eps);
+  const bf16_t* wn = head < Hq ? qn : kn;
+  const float y1 = norm_elem(x1, r, bf2f(wn[lane])), y2 = norm_elem(x2, r, bf2f(wn[lane + 64]));
+  const float c1 = bf2f(cos_t[rpos * 128 + lane]), c2 = bf2f(cos_t[rpos * 128 + lane + 64]);
+  const float s1 = bf2f(sin_t[rpos * 128 + lane]), s2 = bf2f(sin_t[rpos * 128 + lane + 64]);
+  const uint32_t o1 = f2bf(rbf(y1 * c1) + rbf(-y2 * s1));
+  const uint32_t o2 = f2bf(rbf(y2 * c2) + rbf(y1 * s2));
+  bf16_t* dst;
+  if (head < Hq) {
+    dst = q_out + (row * Hq + head) * 128;  // q_out [B, T, Hq, 128]
+  } else {
+    if (slot < 0 || slot >= cap) return;
+    dst = k_cache + ((b * Hkv + (head - Hq)) * cap + slot) * 128;
+  }
+  dst[lane] = (bf16_t)o1;
+  dst[lane + 64] = (bf16_t)o2;
+}
+
+void launch_qk_norm_rope(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn, const bf16_t* kn,
+                         const bf16_t* cos_t, const bf16_t* sin_t, int64_t table_len,
+                         const int64_t* pos, const int64_t* depth, int mode, bf16_t* q_out,
+                         bf16_t* k_cache, bf16_t* v_cache, int64_t B, int64_t T, int Hq, int Hkv,
+                         int64_t cap, float eps, hipStream_t s) {
+  if (B * T <= 0) return;
+  qk_norm_rope_kernel<<<dim3((unsigned)(B * T), (unsigned)(Hq + 2 * Hkv)), dim3(64), 0, s>>>(
+      qkv, qkv_stride, qn, kn, cos_t, sin_t, table_len, pos, depth, mode, q_out, k_cache, v_cache,
+      T, Hq, Hkv, cap, eps);
+}
+
+// ------------------------------------------------------------------ SwiGLU
+// act = bf16(bf16(silu(g)) * u) from packed [rows, 2*inter] (gate | up) (fused.py:101-110,
+// TF:modeling_qwen3.py:81-83).
+__global__ __launch_bounds__(256) void swiglu_kernel(const bf16_t* __restrict__ gu,
+                                                     int64_t gu_stride, bf16_t* __restrict__ out,
+                                                     int64_t out_stride, int64_t inter) {
+  const int64_t row = blockIdx.y;
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= inter / 8) return;
+  const uint4 g = reinterpret_cast<const uint4*>(gu + row * gu_stride)[c];
+  const uint4 u = reinterpret_cast<const uint4*>(gu + row * gu_stride + inter)[c];
+  uint4 o;
+#define SW(lo, hi, G, U) pack2(rbf(silu_f(lo(G))) * lo(U), rbf(silu_f(hi(G))) * hi(U))
+  o.x = SW(bflo, bfhi, g.x, u.x);
+  o.y = SW(bflo, bfhi, g.y, u.y);
+  o.z = SW(bflo, bfhi, g.z, u.z);
+  o.w = SW(bflo, bfhi, g.w, u.w);
+#undef SW
+  reinterpret_cast<uint4*>(out + row * out_stride)[c] = o;
+}
+
+void launch_swiglu(const bf16_t* gu, int64_t gu_stride, bf16_t* out, int64_t out_stride,
+                   int64_t rows, int64_t inter, hipStream_t s) {
+  if (rows <= 0) return;
+  const unsigned gx = (unsigned)((inter / 8 + 255) / 256);
+  swiglu_kernel<<<dim3(gx, (unsigned)rows), dim3(256), 0, s>>>(gu, gu_stride, out, out_stride,
+                                                                inter);
+}
+
+// ------------------------------------------------------------------ KV compaction
+// For the accepted tree path of row b (tree.py:145-164): for k = 1 .. cnt[b]-1,
+// cache[base + k] <- cache[base + src[b, k]] in every layer, for K and V.  src[k] >= k, and
+// each thread moves the same (head, 8-dim) position of every slot, so the in-order per-thread
+// loop never reads a slot after it was overwritten.
+__global__ __launch_bounds__(256) void kv_compact_kernel(bf16_t* k_all, bf16_t* v_all, int64_t B,
+                                                         int Hkv, int64_t cap,
+                                                         const int64_t* __restrict__ base,
+                                                         const int32_t* __restrict__ src,
+                                                         const int32_t* __restrict__ cnt,
+                                                         int64_t T) {
+  const int64_t layer = blockIdx.x, b = blockIdx.y;
+  const int n = cnt[b];
+  const int64_t bs = base[b];
+  const int per = Hkv * 16;  // uint4 chunks per slot per tensor
+  for (int c = threadIdx.x; c < 2 * per; c += blockDim.x) {
+    bf16_t* buf = c < per ? k_all : v_all;
+    const int cc = c < per ? c : c - per;
+    const int h = cc / 16, d8 = cc % 16;
+    uint4* head_base = reinterpret_cast<uint4*>(buf + (((layer * B + b) * Hkv + h) * cap) * 128);
+    for (int k = 1; k < n && k < T; ++k) {
+      const int sidx = src[b * T + k];
+      if (sidx == k || sidx < 0 || sidx >= T) continue;
+      const int64_t from = bs + sidx, to = bs + k;
+      if (from >= cap || to >= cap) continue;
+      head_base[to * 16 + d8] = head_base[from * 16 + d8];
+    }
+  }
+}
+
+void launch_kv_compact(bf16_t* k_all, bf16_t* v_all, int64_t L, int64_t B, int Hkv, int64_t cap,
+                       const int64_t* base, const int32_t* src, const int32_t* cnt, int64_t T,
+                       hipStream_t s) {
+  if (L <= 0 || B <= 0) return;
+  kv_compact_kernel<<<dim3((unsigned)L, (unsigned)B), dim3(256), 0, s>>>(k_all, v_all, B, Hkv,
+                                                                           cap, base, src, cnt, T);
+}
+
+// ------------------------------------------------------------------ synthetic weights
+// Counter-based generator (no reference counterpart: synthetic benchmark data).
+//   h_w(i) = mix64(key + (2 i + w + 1) * 0x9E3779B97F4A7C15), key = seed << 32 | stream
+//   value  = bf16_rne(float(sum of the 16-bit fields of h_0, h_1 - 262140) * scale)
+// Integer arithmetic and one fp32 multiply, so the CPU restatement produces identical bits.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ int64_t fields16(uint64_t h) {
+  return (int64_t)((h & 0xFFFF) + ((h >> 16) & 0xFFFF) + ((h >> 32) & 0xFFFF) + (h >> 48));
+}
+__device__ __forceinline__ uint32_t synth_one(uint64_t key, uint64_t i, float scale) {
+  const uint64_t g = 0x9E3779B97F4A7C15ull;
+  const uint64_t h0 = mix64(key + (2 * i + 1) * g);
+  const uint64_t h1 = mix64(key + (2 * i + 2) * g);
+  const float v = __fmul_rn((float)(fields16(h0) + fields16(h1) - 262140), scale);
+  return f2bf(v);
+}
+
+__global__ __launch_bounds__(256) void synth_kernel(bf16_t* __restrict__ out, int64_t count,
+                                                    uint64_t key, uint64_t start, float scale) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 8 elements per thread
+  const int64_t j0 = c * 8;
+  if (j0 >= count) return;
+  if (j0 + 8 <= count) {
+    uint32_t v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = synth_one(key, start + (uint64_t)(j0 + e), scale);
+    reinterpret_cast<uint4*>(out)[c] =
+        make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16));
+  } else {
+    for (int64_t j = j0; j < count; ++j) out[j] = (bf16_t)synth_one(key, start + (uint64_t)j, scale);
+  }
+}
+
+void launch_synth(bf16_t* out, int64_t count, uint64_t seed, uint64_t stream, uint64_t start,
+                  float scale, hipStream_t s) {
+  if (count <= 0) return;
+  const int64_t threads = (count + 7) / 8;
+  const uint64_t key = (seed << 32) | stream;
+  synth_kernel<<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(out, count, key, start,
+                                                                             scale);
+}
+
+__global__ __launch_bounds__(256) void fill_kernel(bf16_t* out, int64_t count, uint16_t value) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < count) out[i] = value;
+}
+
+void launch_fill(bf16_t* out, int64_t count, uint16_t value, hipStream_t s) {
+  if (count <= 0) return;
+  fill_kernel<<<dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s>>>(out, count, value);
+}
+
+// ------------------------------------------------------------------ greedy argmax reduction
+// tok[m] = index of the maximum over the per-tile (value, lowest index) partials of row m,
+// lowest index on exact ties (gemv.py:147-154, fast.py:402-426); optionally pos[0] += 1.
+__global__ __launch_bounds__(256) void argmax_reduce_kernel(const float* __restrict__ pval,
+                                                            const int32_t* __restrict__ pidx,
+                                                            int64_t nparts, int64_t* tok,
+                                                            int64_t* pos_inc) {
+  __shared__ float sv[256];
+  __shared__ int32_t si[256];
+  const int64_t m = blockIdx.x;
+  float bv = -INFINITY;
+  int32_t bi = 0x7FFFFFFF;
+  for (int64_t p = threadIdx.x; p < nparts; p += 256) {
+    const float v = pval[m * nparts + p];
+    const int32_t i = pidx[m * nparts + p];
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+  }
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (threadIdx.x < off) {
+      const float v = sv[threadIdx.x + off];
+      const int32_t i = si[threadIdx.x + off];
+      if (v > sv[threadIdx.x] || (v == sv[threadIdx.x] && i < si[threadIdx.x])) {
+        sv[threadIdx.x] = v;
+        si[threadIdx.x] = i;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    tok[m] = si[0] == 0x7FFFFFFF ? 0 : (int64_t)si[0];
+    if (pos_inc && m == 0) pos_inc[0] += 1;
+  }
+}
+
+void launch_argmax_reduce(const float* pval, const int32_t* pidx, int64_t nparts, int64_t M,
+                          int64_t* tok, int64_t* pos_inc, hipStream_t s) {
+  if (M <= 0) return;
+  argmax_reduce_kernel<<<dim3((unsigned)M), dim3(256), 0, s>>>(pval, pidx, nparts, tok, pos_inc);
+}

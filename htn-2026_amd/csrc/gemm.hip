@@ -1,0 +1,161 @@
+// MFMA decode / verify / prefill GEMM:  out[m, n] = epi( sum_k X[m, k] * W[n, k] )
+// for any number of activation rows M (batched decode B >= 3, tree verification B*T rows,
+// chunked prefill), with the same epilogues as the vector path plus a per-tile argmax for the
+// LM head (gemv.py:61-116, fast.py:99-213, gemv.py:118-154).
+//
+// CDNA4 mapping (v_mfma_f32_16x16x32_bf16, wave64):
+//  * a workgroup owns 16 weight rows (one MFMA N tile) and up to 64 activation rows (MT M tiles);
+//    its NW waves split K round-robin in groups of 128 and are summed in LDS at the end;
+//  * lane (q = lane / 16, c = lane % 16) streams 64 contiguous bytes of weight row n0 + c per
+//    group (k = g*128 + 32 q .. +31) and the same k range of activation row m0 + 16 mt + c; the
+//    four 16-byte pieces feed four MFMAs.  The k order inside a group is a permutation shared by
+//    both operands, so the contraction is unchanged;
+//  * grid.x walks the M blocks fastest, so the workgroups that re-read one weight tile for
+//    different M blocks run together and hit L2 / MALL instead of HBM.
+// Accumulation is fp32; only the summation order differs from the reference.
+#include "qd_launch.h"
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+__device__ __forceinline__ bf16x8_t as_bf8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+template <int MT, int EPI, int NW>
+__global__ __launch_bounds__(NW * 64) void gemm_kernel(
+    const bf16_t* __restrict__ X, int64_t x_stride, int M, const bf16_t* __restrict__ W, int N,
+    int K, bf16_t* out, int64_t out_stride, const bf16_t* res, int64_t res_stride, float* pval,
+    int32_t* pidx, float* logits) {
+  constexpr bool SW = EPI == EPI_SWIGLU;
+  __shared__ float red[NW][MT * 256];
+  __shared__ float red2[SW ? NW : 1][SW ? MT * 256 : 1];
+  __shared__ float tile[EPI == EPI_ARGMAX ? MT * 16 : 1][17];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = lane & 15, q = lane >> 4;
+  const int64_t m0 = (int64_t)blockIdx.x * (MT * 16);
+  const int64_t n0 = (int64_t)blockIdx.y * 16;
+  const int64_t nrow = n0 + c < N ? n0 + c : N - 1;  // clamped rows are computed, never stored
+  const uint4* wr = reinterpret_cast<const uint4*>(W + nrow * K);
+  const uint4* wr2 = reinterpret_cast<const uint4*>(W + (nrow + (SW ? N : 0)) * K);
+  const uint4* xr[MT];
+  bool xok[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int64_t m = m0 + mt * 16 + c;
+    xok[mt] = m < M;
+    xr[mt] = reinterpret_cast<const uint4*>(X + (xok[mt] ? m : 0) * x_stride);
+  }
+  f32x4_t acc[MT], acc2[SW ? MT : 1];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if constexpr (SW) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc2[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const int ngroups = K / 128;
+  for (int g = wave; g < ngroups; g += NW) {
+    const int64_t c0 = (int64_t)g * 16 + q * 4;  // uint4 index of k = g*128 + 32 q
+    uint4 wv[4], wv2[SW ? 4 : 1];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) wv[s] = ld_stream(wr + c0 + s);
+    if constexpr (SW) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) wv2[s] = ld_stream(wr2 + c0 + s);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      uint4 xv[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xv[s] = xok[mt] ? xr[mt][c0 + s] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xv[s]), as_bf8(wv[s]), acc[mt], 0, 0, 0);
+        if constexpr (SW)
+          acc2[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xv[s]), as_bf8(wv2[s]), acc2[mt], 0, 0, 0);
+      }
+    }
+  }
+  // D[i][j] of one 16x16 tile: lane holds rows i = 4 q + r (r < 4) of column j = c
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      red[wave][mt * 256 + lane * 4 + r] = acc[mt][r];
+      if constexpr (SW) red2[wave][mt * 256 + lane * 4 + r] = acc2[mt][r];
+    }
+  __syncthreads();
+  for (int e = threadIdx.x; e < MT * 256; e += NW * 64) {
+    float v = red[0][e];
+#pragma unroll
+    for (int w2 = 1; w2 < NW; ++w2) v += red[w2][e];
+    const int mt = e / 256, ln = (e % 256) / 4, r = e % 4;
+    const int64_t m = m0 + mt * 16 + (ln >> 4) * 4 + r;
+    const int64_t n = n0 + (ln & 15);
+    if constexpr (EPI == EPI_ARGMAX) {
+      const bool ok = m < M && n < N;
+      if (ok && logits) logits[m * (int64_t)N + n] = v;
+      tile[mt * 16 + (ln >> 4) * 4 + r][ln & 15] = ok ? rbf(v) : -INFINITY;
+      continue;
+    }
+    if (m >= M || n >= N) continue;
+    float y;
+    if constexpr (EPI == EPI_RES) {
+      y = bf2f(res[m * res_stride + n]) + rbf(v);
+    } else if constexpr (SW) {
+      float u = red2[0][e];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) u += red2[w2][e];
+      y = rbf(silu_f(rbf(v))) * rbf(u);
+    } else {
+      y = v;
+    }
+    out[m * out_stride + n] = (bf16_t)f2bf(y);
+  }
+  if constexpr (EPI == EPI_ARGMAX) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < MT * 16; i += NW * 64) {
+      const int64_t m = m0 + i;
+      if (m >= M) continue;
+      float bv = -INFINITY;
+      int32_t bi = 0x7FFFFFFF;
+      for (int j = 0; j < 16; ++j) {
+        const float v = tile[i][j];
+        if (v > bv) { bv = v; bi = (int32_t)(n0 + j); }  // ascending n: strict > keeps lowest
+      }
+      pval[m * (int64_t)gridDim.y + blockIdx.y] = bv;
+      pidx[m * (int64_t)gridDim.y + blockIdx.y] = bi;
+    }
+  }
+}
+
+int64_t gemm_argmax_parts(int64_t N) { return (N + 15) / 16; }
+
+template <int MT, int EPI>
+static void gemm_go(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N, int64_t K,
+                    bf16_t* out, int64_t os, const bf16_t* res, int64_t rs, float* pval,
+                    int32_t* pidx, float* logits, hipStream_t s) {
+  constexpr int NW = 4;
+  const dim3 grid((unsigned)((M + MT * 16 - 1) / (MT * 16)), (unsigned)((N + 15) / 16));
+  gemm_kernel<MT, EPI, NW><<<grid, dim3(NW * 64), 0, s>>>(x, xs, (int)M, w, (int)N, (int)K, out, os,
+                                                         res, rs, pval, pidx, logits);
+}
+
+template <int EPI>
+static void gemm_mt(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N, int64_t K,
+                    bf16_t* out, int64_t os, const bf16_t* res, int64_t rs, float* pval,
+                    int32_t* pidx, float* logits, hipStream_t s) {
+  if (M <= 16) gemm_go<1, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
+  else if (M <= 32) gemm_go<2, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
+  else gemm_go<4, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
+}
+
+void launch_gemm(const bf16_t* x, int64_t x_stride, int64_t M, const bf16_t* w, int64_t N,
+                 int64_t K, bf16_t* out, int64_t out_stride, const bf16_t* res, int64_t res_stride,
+                 int epi, float* pval, int32_t* pidx, float* logits, hipStream_t s) {
+  if (M <= 0) return;
+  switch (epi) {
+    case EPI_RES: gemm_mt<EPI_RES>(x, x_stride, M, w, N, K, out, out_stride, res, res_stride, pval, pidx, logits, s); break;
+    case EPI_SWIGLU: gemm_mt<EPI_SWIGLU>(x, x_stride, M, w, N, K, out, out_stride, res, res_stride, pval, pidx, logits, s); break;
+    case EPI_ARGMAX: gemm_mt<EPI_ARGMAX>(x, x_stride, M, w, N, K, out, out_stride, res, res_stride, pval, pidx, logits, s); break;
+    default: gemm_mt<EPI_NONE>(x, x_stride, M, w, N, K, out, out_stride, res, res_stride, pval, pidx, logits, s); break;
+  }
+}

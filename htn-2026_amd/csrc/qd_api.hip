@@ -1,0 +1,451 @@
+// extern "C" entry points (include/qdecode.h): argument validation, workspace layout and the
+// whole-step launch sequences.  Kernels live in elementwise.hip, gemv.hip, gemm.hip, attn.hip.
+#include "../../include/qdecode.h"
+
+#include <string.h>
+
+#include "qd_launch.h"
+
+namespace {
+
+inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int launched() { return qd_err(hipGetLastError()); }
+
+inline int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
+
+// Carves consecutive 256-byte-aligned regions out of a workspace.
+struct Carver {
+  char* base;
+  int64_t off = 0;
+  explicit Carver(void* p) : base(static_cast<char*>(p)) {}
+  template <typename T>
+  T* take(int64_t count) {
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off += align256(count * (int64_t)sizeof(T));
+    return p;
+  }
+};
+
+struct AttnWs {
+  float* acc;
+  float* ml;
+  int* tickets;
+};
+AttnWs carve_decode_attn(Carver& c, int64_t B, int64_t Hq, int64_t Hkv, int64_t splits) {
+  AttnWs a;
+  a.acc = c.take<float>(B * Hq * splits * 128);
+  a.ml = c.take<float>(B * Hq * splits * 2);
+  a.tickets = c.take<int>(B * Hkv);
+  return a;
+}
+
+struct LmWs {
+  float* val;
+  int32_t* idx;
+  int* ticket;
+  bf16_t* xn;
+  int64_t parts;
+};
+LmWs carve_lm(Carver& c, int64_t rows, int64_t V, int64_t K) {
+  LmWs l;
+  const bool vec = gemv_supported(rows, K) && K == 2560;
+  l.parts = vec ? lm_vec_parts(V) : gemm_argmax_parts(V);
+  l.val = c.take<float>(rows * l.parts);
+  l.idx = c.take<int32_t>(rows * l.parts);
+  l.ticket = c.take<int>(1);
+  l.xn = vec ? nullptr : c.take<bf16_t>(rows * K);
+  return l;
+}
+
+// LM head + argmax over `rows` rows of x (row stride x_stride)
+int lm_head(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t V, int64_t K,
+            int64_t rows, const bf16_t* norm_w, float eps, int64_t* tok, int64_t* pos_inc,
+            float* logits, const LmWs& l, hipStream_t s) {
+  if (gemv_supported(rows, K) && K == 2560) {
+    launch_lm_vec(x, x_stride, w, V, K, norm_w, eps, rows, l.val, l.idx, l.ticket, tok, pos_inc,
+                  logits, s);
+  } else {
+    launch_add_rmsnorm(nullptr, x, norm_w, nullptr, l.xn, rows, K, x_stride, K, eps, s);
+    launch_gemm(l.xn, K, rows, w, V, K, nullptr, 0, nullptr, 0, EPI_ARGMAX, l.val, l.idx, logits, s);
+    launch_argmax_reduce(l.val, l.idx, l.parts, rows, tok, pos_inc, s);
+  }
+  return launched();
+}
+
+bool weights_ok(const qd_weights* w) {
+  if (!w || !w->embed || !w->final_norm || !w->w_qkv || !w->w_o || !w->w_gu || !w->w_down ||
+      !w->ln1 || !w->ln2 || !w->q_norm || !w->k_norm)
+    return false;
+  if (w->n_layers <= 0 || w->head_dim != 128 || w->n_kv_heads <= 0 ||
+      w->n_q_heads != 4 * w->n_kv_heads || w->vocab <= 0)
+    return false;
+  if (w->hidden % 128 || w->inter % 128 || (w->n_q_heads * 128) % 128) return false;
+  return true;
+}
+
+inline int64_t qkv_width(const qd_weights* w) { return (int64_t)(w->n_q_heads + 2 * w->n_kv_heads) * 128; }
+
+}  // namespace
+
+extern "C" {
+
+const char* qd_version(void) { return "qdecode 0.1 gfx950"; }
+
+int qd_embed_gather(const int64_t* ids, const uint16_t* table, uint16_t* out, int64_t n_ids,
+                    int64_t vocab, int64_t hidden, int64_t out_stride, void* stream) {
+  if (n_ids < 0 || vocab <= 0 || hidden <= 0 || hidden % 8 || out_stride < hidden || out_stride % 8)
+    return QD_EARG;
+  if (n_ids == 0) return QD_OK;
+  if (!ids || !table || !out) return QD_EARG;
+  launch_embed(ids, table, out, n_ids, vocab, hidden, out_stride, S(stream));
+  return launched();
+}
+
+int qd_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* w,
+                   uint16_t* res_out, uint16_t* y, int64_t rows, int64_t hidden, int64_t in_stride,
+                   int64_t y_stride, float eps, void* stream) {
+  if (rows < 0 || hidden <= 0 || hidden % 8 || in_stride < hidden || in_stride % 8 ||
+      y_stride < hidden || y_stride % 8 || !(eps >= 0.f))
+    return QD_EARG;
+  if (rows == 0) return QD_OK;
+  if (!residual || !w || !y || (x && !res_out)) return QD_EARG;
+  launch_add_rmsnorm(x, residual, w, res_out, y, rows, hidden, in_stride, y_stride, eps, S(stream));
+  return launched();
+}
+
+int qd_qk_norm_rope(const uint16_t* qkv, int64_t qkv_stride, const uint16_t* q_norm_w,
+                    const uint16_t* k_norm_w, const uint16_t* cos, const uint16_t* sin,
+                    int64_t table_len, const int64_t* pos, const int64_t* depth, int32_t mode,
+                    uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int64_t batch,
+                    int64_t T, int64_t n_q_heads, int64_t n_kv_heads, int64_t cap, float eps,
+                    void* stream) {
+  if (batch < 0 || T < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || cap <= 0 || table_len <= 0)
+    return QD_EARG;
+  if (qkv_stride < (n_q_heads + 2 * n_kv_heads) * 128) return QD_EARG;
+  if (mode < QD_POS_T || mode > QD_POS_TREE) return QD_EARG;
+  if (batch * T == 0) return QD_OK;
+  if (!qkv || !q_norm_w || !k_norm_w || !cos || !sin || !q_out || !k_cache || !v_cache)
+    return QD_EARG;
+  if (mode != QD_POS_T && !pos) return QD_EARG;
+  if (mode == QD_POS_TREE && !depth) return QD_EARG;
+  launch_qk_norm_rope(qkv, qkv_stride, q_norm_w, k_norm_w, cos, sin, table_len, pos, depth, mode,
+                      q_out, k_cache, v_cache, batch, T, (int)n_q_heads, (int)n_kv_heads, cap, eps,
+                      S(stream));
+  return launched();
+}
+
+int qd_swiglu(const uint16_t* gu, int64_t gu_stride, uint16_t* out, int64_t out_stride,
+              int64_t rows, int64_t inter, void* stream) {
+  if (rows < 0 || inter <= 0 || inter % 8 || gu_stride < 2 * inter || gu_stride % 8 ||
+      out_stride < inter || out_stride % 8)
+    return QD_EARG;
+  if (rows == 0) return QD_OK;
+  if (!gu || !out) return QD_EARG;
+  launch_swiglu(gu, gu_stride, out, out_stride, rows, inter, S(stream));
+  return launched();
+}
+
+int64_t qd_linear_workspace_bytes(int64_t rows, int64_t k, int32_t has_norm) {
+  if (rows <= 0 || k <= 0) return 0;
+  if (gemv_supported(rows, k) || !has_norm) return 0;
+  return align256(rows * k * 2);
+}
+
+int qd_linear(const uint16_t* x, int64_t x_stride, const uint16_t* w, int64_t n_out, int64_t k,
+              uint16_t* out, int64_t out_stride, int64_t rows, const uint16_t* norm_w, float eps,
+              int32_t epilogue, const uint16_t* res, int64_t res_stride, void* workspace,
+              int64_t workspace_bytes, void* stream) {
+  if (rows < 0 || n_out <= 0 || k <= 0 || k % 128 || x_stride < k || x_stride % 8) return QD_EARG;
+  if (epilogue < QD_EPI_NONE || epilogue > QD_EPI_SWIGLU) return QD_EARG;
+  if (rows == 0) return QD_OK;
+  if (!x || !w || !out) return QD_EARG;
+  if (epilogue == QD_EPI_RES && !res) return QD_EARG;
+  hipStream_t s = S(stream);
+  if (gemv_supported(rows, k)) {
+    launch_gemv(x, x_stride, w, n_out, k, out, out_stride, res, res_stride, norm_w, eps, epilogue,
+                rows, s);
+    return launched();
+  }
+  const bf16_t* xin = x;
+  int64_t xin_stride = x_stride;
+  if (norm_w) {
+    const int64_t need = qd_linear_workspace_bytes(rows, k, 1);
+    if (!workspace || workspace_bytes < need) return QD_EWS;
+    bf16_t* xn = static_cast<bf16_t*>(workspace);
+    launch_add_rmsnorm(nullptr, x, norm_w, nullptr, xn, rows, k, x_stride, k, eps, s);
+    xin = xn;
+    xin_stride = k;
+  }
+  launch_gemm(xin, xin_stride, rows, w, n_out, k, out, out_stride, res, res_stride, epilogue,
+              nullptr, nullptr, nullptr, s);
+  return launched();
+}
+
+int64_t qd_lm_head_workspace_bytes(int64_t rows, int64_t vocab, int64_t k) {
+  if (rows <= 0 || vocab <= 0 || k <= 0) return 0;
+  Carver c(nullptr);
+  carve_lm(c, rows, vocab, k);
+  return c.off;
+}
+
+int qd_lm_head_argmax(const uint16_t* x, int64_t x_stride, const uint16_t* w, int64_t vocab,
+                      int64_t k, int64_t rows, const uint16_t* norm_w, float eps, int64_t* tok,
+                      int64_t* pos_inc, float* logits, void* workspace, int64_t workspace_bytes,
+                      void* stream) {
+  if (rows < 0 || vocab <= 0 || vocab >= 0x7FFFFFFF || k <= 0 || k % 128 || x_stride < k ||
+      x_stride % 8)
+    return QD_EARG;
+  if (rows == 0) return QD_OK;
+  if (!x || !w || !norm_w || !tok) return QD_EARG;
+  if (!workspace || workspace_bytes < qd_lm_head_workspace_bytes(rows, vocab, k)) return QD_EWS;
+  Carver c(workspace);
+  LmWs l = carve_lm(c, rows, vocab, k);
+  return lm_head(x, x_stride, w, vocab, k, rows, norm_w, eps, tok, pos_inc, logits, l, S(stream));
+}
+
+int64_t qd_decode_attn_workspace_bytes(int64_t batch, int64_t n_q_heads, int64_t n_kv_heads,
+                                       int64_t cap) {
+  if (batch <= 0 || n_kv_heads <= 0 || cap <= 0) return 0;
+  Carver c(nullptr);
+  carve_decode_attn(c, batch, n_q_heads, n_kv_heads, decode_attn_splits(batch, (int)n_kv_heads, cap));
+  return c.off;
+}
+
+int qd_decode_attn(const uint16_t* qkv, int64_t qkv_stride, const uint16_t* q_norm_w,
+                   const uint16_t* k_norm_w, const uint16_t* cos, const uint16_t* sin,
+                   const int64_t* pos, uint16_t* k_cache, uint16_t* v_cache, int64_t batch,
+                   int64_t n_q_heads, int64_t n_kv_heads, int64_t cap, float eps, uint16_t* out,
+                   void* workspace, int64_t workspace_bytes, void* stream) {
+  if (batch < 0 || n_kv_heads <= 0 || n_q_heads != 4 * n_kv_heads || cap <= 0 ||
+      qkv_stride < (n_q_heads + 2 * n_kv_heads) * 128)
+    return QD_EARG;
+  if (batch == 0) return QD_OK;
+  if (!qkv || !q_norm_w || !k_norm_w || !cos || !sin || !pos || !k_cache || !v_cache || !out)
+    return QD_EARG;
+  if (!workspace || workspace_bytes < qd_decode_attn_workspace_bytes(batch, n_q_heads, n_kv_heads, cap))
+    return QD_EWS;
+  const int64_t splits = decode_attn_splits(batch, (int)n_kv_heads, cap);
+  Carver c(workspace);
+  AttnWs a = carve_decode_attn(c, batch, n_q_heads, n_kv_heads, splits);
+  launch_decode_attn(qkv, qkv_stride, q_norm_w, k_norm_w, cos, sin, pos, k_cache, v_cache, batch,
+                     (int)n_q_heads, (int)n_kv_heads, cap, splits, eps, a.acc, a.ml, a.tickets,
+                     out, S(stream));
+  return launched();
+}
+
+int64_t qd_block_attn_workspace_bytes(int64_t batch, int64_t T, int64_t n_q_heads, int64_t cap) {
+  if (batch <= 0 || T <= 0 || cap <= 0) return 0;
+  const int64_t rows = batch * T * n_q_heads * block_attn_splits(cap);
+  return align256(rows * 128 * 4) + align256(rows * 2 * 4);
+}
+
+int qd_block_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                  const int64_t* base, const uint64_t* anc, int64_t batch, int64_t T,
+                  int64_t n_q_heads, int64_t n_kv_heads, int64_t cap, uint16_t* out,
+                  void* workspace, int64_t workspace_bytes, void* stream) {
+  if (batch < 0 || T < 0 || n_kv_heads <= 0 || n_q_heads != 4 * n_kv_heads || cap <= 0) return QD_EARG;
+  if (anc && T > 64) return QD_EARG;
+  if (batch * T == 0) return QD_OK;
+  if (!q || !k_cache || !v_cache || !base || !out) return QD_EARG;
+  if (!workspace || workspace_bytes < qd_block_attn_workspace_bytes(batch, T, n_q_heads, cap))
+    return QD_EWS;
+  const int64_t splits = block_attn_splits(cap);
+  Carver c(workspace);
+  const int64_t rows = batch * T * n_q_heads * splits;
+  float* acc = c.take<float>(rows * 128);
+  float* ml = c.take<float>(rows * 2);
+  launch_block_attn(q, k_cache, v_cache, base, anc, batch, T, (int)n_q_heads, (int)n_kv_heads, cap,
+                    splits, acc, ml, out, S(stream));
+  return launched();
+}
+
+int qd_kv_compact(uint16_t* k_all, uint16_t* v_all, int64_t n_layers, int64_t batch,
+                  int64_t n_kv_heads, int64_t cap, const int64_t* base, const int32_t* src,
+                  const int32_t* cnt, int64_t T, void* stream) {
+  if (n_layers < 0 || batch < 0 || n_kv_heads <= 0 || cap <= 0 || T <= 0) return QD_EARG;
+  if (n_layers * batch == 0) return QD_OK;
+  if (!k_all || !v_all || !base || !src || !cnt) return QD_EARG;
+  launch_kv_compact(k_all, v_all, n_layers, batch, (int)n_kv_heads, cap, base, src, cnt, T, S(stream));
+  return launched();
+}
+
+int qd_synth_bf16(uint16_t* out, int64_t count, uint64_t seed, uint64_t stream, uint64_t start,
+                  float scale, void* stream_) {
+  if (count < 0 || seed > 0xFFFFFFFFull || stream > 0xFFFFFFFFull) return QD_EARG;
+  if (count == 0) return QD_OK;
+  if (!out || (reinterpret_cast<uintptr_t>(out) & 15)) return QD_EARG;
+  launch_synth(out, count, seed, stream, start, scale, S(stream_));
+  return launched();
+}
+
+int qd_fill_bf16(uint16_t* out, int64_t count, uint16_t value, void* stream) {
+  if (count < 0) return QD_EARG;
+  if (count == 0) return QD_OK;
+  if (!out) return QD_EARG;
+  launch_fill(out, count, value, S(stream));
+  return launched();
+}
+
+// ------------------------------------------------------------------ decode step
+int64_t qd_decode_workspace_bytes(const qd_weights* w, int64_t batch, int64_t cap) {
+  if (!w || batch <= 0 || cap <= 0) return 0;
+  Carver c(nullptr);
+  carve_decode_attn(c, batch, w->n_q_heads, w->n_kv_heads, decode_attn_splits(batch, w->n_kv_heads, cap));
+  carve_lm(c, batch, w->vocab, w->hidden);
+  c.take<bf16_t>(batch * (int64_t)w->hidden);  // normalised activations (MFMA path)
+  return c.off;
+}
+
+int qd_decode_step(const qd_weights* w, const qd_decode_state* st, void* stream) {
+  if (!weights_ok(w) || !st) return QD_EARG;
+  const int64_t B = st->batch, cap = st->cap, H = w->hidden, I = w->inter, V = w->vocab;
+  const int Hq = w->n_q_heads, Hkv = w->n_kv_heads;
+  if (B <= 0 || cap <= 0 || !st->k_cache || !st->v_cache || !st->cos || !st->sin || !st->tok ||
+      !st->pos || !st->x || !st->qkv || !st->attn || !st->act)
+    return QD_EARG;
+  if (!st->workspace || st->workspace_bytes < qd_decode_workspace_bytes(w, B, cap)) return QD_EWS;
+  hipStream_t s = S(stream);
+  const int64_t splits = decode_attn_splits(B, Hkv, cap);
+  Carver c(st->workspace);
+  AttnWs aw = carve_decode_attn(c, B, Hq, Hkv, splits);
+  LmWs lw = carve_lm(c, B, V, H);
+  bf16_t* xn = c.take<bf16_t>(B * H);
+  const int64_t NQKV = qkv_width(w), QD = (int64_t)Hq * 128;
+  const int64_t layer_kv = B * Hkv * cap * 128;
+  const bool vec_h = gemv_supported(B, H), vec_q = gemv_supported(B, QD), vec_i = gemv_supported(B, I);
+
+  launch_embed(st->tok, w->embed, st->x, B, V, H, H, s);
+  for (int64_t l = 0; l < w->n_layers; ++l) {
+    const bf16_t* wqkv = w->w_qkv + l * NQKV * H;
+    const bf16_t* wo = w->w_o + l * H * QD;
+    const bf16_t* wgu = w->w_gu + l * 2 * I * H;
+    const bf16_t* wd = w->w_down + l * H * I;
+    const bf16_t* ln1 = w->ln1 + l * H;
+    const bf16_t* ln2 = w->ln2 + l * H;
+    // qkv = RMSNorm(x; ln1) . Wqkv
+    if (vec_h) {
+      launch_gemv(st->x, H, wqkv, NQKV, H, st->qkv, NQKV, nullptr, 0, ln1, w->eps, EPI_NONE, B, s);
+    } else {
+      launch_add_rmsnorm(nullptr, st->x, ln1, nullptr, xn, B, H, H, H, w->eps, s);
+      launch_gemm(xn, H, B, wqkv, NQKV, H, st->qkv, NQKV, nullptr, 0, EPI_NONE, nullptr, nullptr, nullptr, s);
+    }
+    // attention (q/k norm + RoPE + KV write + split-K + merge)
+    launch_decode_attn(st->qkv, NQKV, w->q_norm + l * 128, w->k_norm + l * 128, st->cos, st->sin,
+                       st->pos, st->k_cache + l * layer_kv, st->v_cache + l * layer_kv, B, Hq, Hkv,
+                       cap, splits, w->eps, aw.acc, aw.ml, aw.tickets, st->attn, s);
+    // x = x + attn . Wo
+    if (vec_q)
+      launch_gemv(st->attn, QD, wo, H, QD, st->x, H, st->x, H, nullptr, 0.f, EPI_RES, B, s);
+    else
+      launch_gemm(st->attn, QD, B, wo, H, QD, st->x, H, st->x, H, EPI_RES, nullptr, nullptr, nullptr, s);
+    // act = SwiGLU(RMSNorm(x; ln2) . Wgu)
+    if (vec_h) {
+      launch_gemv(st->x, H, wgu, I, H, st->act, I, nullptr, 0, ln2, w->eps, EPI_SWIGLU, B, s);
+    } else {
+      launch_add_rmsnorm(nullptr, st->x, ln2, nullptr, xn, B, H, H, H, w->eps, s);
+      launch_gemm(xn, H, B, wgu, I, H, st->act, I, nullptr, 0, EPI_SWIGLU, nullptr, nullptr, nullptr, s);
+    }
+    // x = x + act . Wdown
+    if (vec_i)
+      launch_gemv(st->act, I, wd, H, I, st->x, H, st->x, H, nullptr, 0.f, EPI_RES, B, s);
+    else
+      launch_gemm(st->act, I, B, wd, H, I, st->x, H, st->x, H, EPI_RES, nullptr, nullptr, nullptr, s);
+  }
+  return lm_head(st->x, H, w->embed, V, H, B, w->final_norm, w->eps, st->tok, st->pos, nullptr, lw, s);
+}
+
+// ------------------------------------------------------------------ block (tree / prefill chunk)
+int64_t qd_block_workspace_bytes(const qd_weights* w, int64_t batch, int64_t T, int64_t cap) {
+  if (!w || batch <= 0 || T <= 0 || cap <= 0) return 0;
+  const int64_t lm_rows = batch * T;  // upper bound (last_only uses batch rows)
+  Carver c(nullptr);
+  const int64_t rows = batch * T * w->n_q_heads * block_attn_splits(cap);
+  c.take<float>(rows * 128);
+  c.take<float>(rows * 2);
+  carve_lm(c, lm_rows, w->vocab, w->hidden);
+  return c.off;
+}
+
+int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
+  if (!weights_ok(w) || !st) return QD_EARG;
+  const int64_t B = st->batch, T = st->T, cap = st->cap, H = w->hidden, I = w->inter, V = w->vocab;
+  const int Hq = w->n_q_heads, Hkv = w->n_kv_heads;
+  if (B <= 0 || T <= 0 || cap <= 0 || !st->k_cache || !st->v_cache || !st->cos || !st->sin ||
+      !st->tokens || !st->base || !st->out_tok || !st->x || !st->xn || !st->qkv || !st->q ||
+      !st->attn || !st->act)
+    return QD_EARG;
+  if (!st->causal && (!st->anc || !st->depth || T > 64)) return QD_EARG;
+  if (!st->workspace || st->workspace_bytes < qd_block_workspace_bytes(w, B, T, cap)) return QD_EWS;
+  hipStream_t s = S(stream);
+  const int64_t M = B * T;
+  const int64_t splits = block_attn_splits(cap);
+  Carver c(st->workspace);
+  const int64_t arows = M * Hq * splits;
+  float* acc = c.take<float>(arows * 128);
+  float* ml = c.take<float>(arows * 2);
+  const int64_t lm_rows = st->last_only ? B : M;
+  LmWs lw = carve_lm(c, lm_rows, V, H);
+  const int64_t NQKV = qkv_width(w), QD = (int64_t)Hq * 128;
+  const int64_t layer_kv = B * Hkv * cap * 128;
+
+  if (st->c_base && st->c_src && st->c_cnt)
+    launch_kv_compact(st->k_cache, st->v_cache, w->n_layers, B, Hkv, cap, st->c_base, st->c_src,
+                      st->c_cnt, T, s);
+  launch_embed(st->tokens, w->embed, st->x, M, V, H, H, s);
+  for (int64_t l = 0; l < w->n_layers; ++l) {
+    bf16_t* kc = st->k_cache + l * layer_kv;
+    bf16_t* vc = st->v_cache + l * layer_kv;
+    launch_add_rmsnorm(nullptr, st->x, w->ln1 + l * H, nullptr, st->xn, M, H, H, H, w->eps, s);
+    launch_gemm(st->xn, H, M, w->w_qkv + l * NQKV * H, NQKV, H, st->qkv, NQKV, nullptr, 0, EPI_NONE,
+                nullptr, nullptr, nullptr, s);
+    launch_qk_norm_rope(st->qkv, NQKV, w->q_norm + l * 128, w->k_norm + l * 128, st->cos, st->sin,
+                        cap, st->base, st->depth, st->causal ? POS_CHUNK : POS_TREE, st->q, kc, vc,
+                        B, T, Hq, Hkv, cap, w->eps, s);
+    launch_block_attn(st->q, kc, vc, st->base, st->causal ? nullptr : st->anc, B, T, Hq, Hkv, cap,
+                      splits, acc, ml, st->attn, s);
+    launch_gemm(st->attn, QD, M, w->w_o + l * H * QD, H, QD, st->x, H, st->x, H, EPI_RES, nullptr,
+                nullptr, nullptr, s);
+    launch_add_rmsnorm(nullptr, st->x, w->ln2 + l * H, nullptr, st->xn, M, H, H, H, w->eps, s);
+    launch_gemm(st->xn, H, M, w->w_gu + l * 2 * I * H, I, H, st->act, I, nullptr, 0, EPI_SWIGLU,
+                nullptr, nullptr, nullptr, s);
+    launch_gemm(st->act, I, M, w->w_down + l * H * I, H, I, st->x, H, st->x, H, EPI_RES, nullptr,
+                nullptr, nullptr, s);
+  }
+  if (st->last_only)
+    return lm_head(st->x + (T - 1) * H, T * H, w->embed, V, H, B, w->final_norm, w->eps,
+                   st->out_tok, nullptr, nullptr, lw, s);
+  return lm_head(st->x, H, w->embed, V, H, M, w->final_norm, w->eps, st->out_tok, nullptr, nullptr,
+                 lw, s);
+}
+
+// ------------------------------------------------------------------ graphs
+int qd_graph_begin(void* stream) {
+  if (!stream) return QD_EARG;  // the legacy null stream cannot be captured
+  return qd_err(hipStreamBeginCapture(S(stream), hipStreamCaptureModeRelaxed));
+}
+
+int qd_graph_end(void* stream, void** exec_out) {
+  if (!stream || !exec_out) return QD_EARG;
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(S(stream), &g);
+  if (e != hipSuccess) return qd_err(e);
+  hipGraphExec_t ex = nullptr;
+  e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return qd_err(e);
+  *exec_out = ex;
+  return QD_OK;
+}
+
+int qd_graph_launch(void* exec, void* stream) {
+  if (!exec) return QD_EARG;
+  return qd_err(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(exec), S(stream)));
+}
+
+int qd_graph_destroy(void* exec) {
+  if (!exec) return QD_OK;
+  return qd_err(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(exec)));
+}
+
+}  // extern "C"

@@ -1,0 +1,63 @@
+// Internal host-side launchers shared between the kernel translation units and the step
+// sequencer.  Every launcher validates nothing (the extern "C" entry points in qd_api.cpp and
+// the step sequencer validate shapes once) and only enqueues on `s`.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qd_common.h"
+
+enum { EPI_NONE = 0, EPI_RES = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
+enum { POS_T = 0, POS_SHARED = 1, POS_ROW = 2, POS_TREE = 3, POS_CHUNK = 4 };
+
+// elementwise.hip
+void launch_embed(const int64_t* ids, const bf16_t* table, bf16_t* out, int64_t n, int64_t vocab,
+                  int64_t hidden, int64_t out_stride, hipStream_t s);
+void launch_add_rmsnorm(const bf16_t* x, const bf16_t* res, const bf16_t* w, bf16_t* res_out,
+                        bf16_t* y, int64_t rows, int64_t hidden, int64_t in_stride, int64_t y_stride,
+                        float eps, hipStream_t s);
+void launch_qk_norm_rope(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn, const bf16_t* kn,
+                         const bf16_t* cos_t, const bf16_t* sin_t, int64_t table_len,
+                         const int64_t* pos, const int64_t* depth, int mode, bf16_t* q_out,
+                         bf16_t* k_cache, bf16_t* v_cache, int64_t B, int64_t T, int Hq, int Hkv,
+                         int64_t cap, float eps, hipStream_t s);
+void launch_swiglu(const bf16_t* gu, int64_t gu_stride, bf16_t* out, int64_t out_stride,
+                   int64_t rows, int64_t inter, hipStream_t s);
+void launch_kv_compact(bf16_t* k_all, bf16_t* v_all, int64_t L, int64_t B, int Hkv, int64_t cap,
+                       const int64_t* base, const int32_t* src, const int32_t* cnt, int64_t T,
+                       hipStream_t s);
+void launch_synth(bf16_t* out, int64_t count, uint64_t seed, uint64_t stream, uint64_t start,
+                  float scale, hipStream_t s);
+void launch_fill(bf16_t* out, int64_t count, uint16_t value, hipStream_t s);
+void launch_argmax_reduce(const float* pval, const int32_t* pidx, int64_t nparts, int64_t M,
+                          int64_t* tok, int64_t* pos_inc, hipStream_t s);
+
+// gemv.hip (vector path, 1..2 rows)
+int gemv_supported(int64_t M, int64_t K);
+void launch_gemv(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t N, int64_t K,
+                 bf16_t* out, int64_t out_stride, const bf16_t* res, int64_t res_stride,
+                 const bf16_t* norm_w, float eps, int epi, int64_t M, hipStream_t s);
+int64_t lm_vec_parts(int64_t V);
+void launch_lm_vec(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t V, int64_t K,
+                   const bf16_t* norm_w, float eps, int64_t M, float* pval, int32_t* pidx,
+                   int* ticket, int64_t* tok, int64_t* pos_inc, float* logits, hipStream_t s);
+
+// gemm.hip (MFMA path, any M)
+int64_t gemm_argmax_parts(int64_t N);
+void launch_gemm(const bf16_t* x, int64_t x_stride, int64_t M, const bf16_t* w, int64_t N,
+                 int64_t K, bf16_t* out, int64_t out_stride, const bf16_t* res, int64_t res_stride,
+                 int epi, float* pval, int32_t* pidx, float* logits, hipStream_t s);
+
+// attn.hip
+int64_t decode_attn_splits(int64_t B, int Hkv, int64_t cap);
+int64_t decode_attn_chunk(int64_t cap, int64_t splits);
+void launch_decode_attn(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn, const bf16_t* kn,
+                        const bf16_t* cos_t, const bf16_t* sin_t, const int64_t* pos,
+                        bf16_t* k_cache, bf16_t* v_cache, int64_t B, int Hq, int Hkv, int64_t cap,
+                        int64_t splits, float eps, float* ws_acc, float* ws_ml, int* tickets,
+                        bf16_t* out, hipStream_t s);
+int64_t block_attn_splits(int64_t cap);
+void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
+                       const int64_t* base, const uint64_t* anc, int64_t B, int64_t T, int Hq,
+                       int Hkv, int64_t cap, int64_t splits, float* ws_acc, float* ws_ml,
+                       bf16_t* out, hipStream_t s);

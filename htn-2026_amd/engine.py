@@ -1,0 +1,176 @@
+"""Qwen3 greedy decode engine for one MI355X -- drop-in for the reference's decode path.
+
+Interface (Yokanater/htn-2026 engine/engine.py:232-293, 1105-1132; QWEN_ENGINE_CONTRACT.md:22-36):
+
+    from engine import Engine               # this directory on sys.path, as the reference's
+    eng = Engine(model_path)                # local HF checkpoint dir (config.json + safetensors)
+    for step in eng.generate(input_ids, max_new_tokens):
+        ...                                 # list of B greedy ids, exactly max_new_tokens times
+
+Semantics kept from the reference: equal-length prompts, no EOS stop, exactly N yields (none
+for N <= 0), prompt state reset on every call, the GPU kept one step ahead of the host with a
+pinned ring and one event per step (engine.py:719-757).  The decode step is the fused T5
+layout (engine.py:463-477) recorded once as a hipGraph; the prompt runs as causal chunks through
+the block forward.  All arithmetic is in libqdecode.so (hand-written gfx950 HIP): there is no
+transformers model, no torch compute and no fallback tier -- a missing library raises at import.
+"""
+
+import gc
+import os
+import sys
+
+import torch
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+
+from qdecode import model as _model  # noqa: E402
+from qdecode import tree as _tree  # noqa: E402
+
+DEVICE = os.environ.get("ENGINE_DEVICE", "cuda:0")
+
+
+class _Shape:
+    """Buffers, runners and graphs for one (B, S, N, mode)."""
+
+    def __init__(self, model, stream, B, S, N, tree_T=0, prefill_rows=None):
+        self.B, self.S, self.N, self.tree_T = B, S, N, tree_T
+        cap = _model.kv_capacity(S, N, extra=tree_T)
+        self.kv = _model.KVState(model, B, cap)
+        self.stream = stream
+        self.chunk = _model.prefill_chunk(B, S, prefill_rows or 4096)
+        self.prefill = _model.BlockRunner(self.kv, stream, self.chunk, causal=True, last_only=True)
+        self.decode = _model.DecodeRunner(self.kv, stream)
+        self.tree = (_model.BlockRunner(self.kv, stream, tree_T, causal=False, last_only=False)
+                     if tree_T else None)
+        self.ids = torch.zeros((B, S), dtype=torch.int64, device=model.device)
+        self.ids_host = torch.empty((B, S), dtype=torch.int64, pin_memory=True)
+        self.host = torch.empty((max(N, 1), B), dtype=torch.int64, pin_memory=True)
+        self.events = [torch.cuda.Event() for _ in range(max(N, 1))]
+        self.graph_ready = False
+
+    def run_prefill(self):
+        """Causal chunks of the prompt: KV [0, S) and the first greedy token into kv.tok."""
+        B, S, c = self.B, self.S, self.chunk
+        pr = self.prefill
+        for c0 in range(0, S, c):
+            T = min(c, S - c0)
+            # the block step reads tokens as [B, T] contiguous
+            pr.tokens.view(-1)[:B * T].view(B, T).copy_(self.ids[:, c0:c0 + T])
+            pr.base.fill_(c0)
+            pr.enqueue(T)
+        self.kv.tok.copy_(pr.out_tok)
+
+
+class Engine:
+    def __init__(self, model_path: str, device: str = DEVICE) -> None:
+        self.device = torch.device(device)
+        torch.cuda.set_device(self.device)
+        self.model = (_model.Qwen3Model.from_checkpoint(model_path, self.device)
+                      if model_path is not None else None)
+        self._init_common()
+
+    @classmethod
+    def synthetic(cls, n_layers=36, seed=1, device=DEVICE):
+        """Engine over seeded random-init weights generated on the device (benchmark configs)."""
+        eng = cls.__new__(cls)
+        eng.device = torch.device(device)
+        torch.cuda.set_device(eng.device)
+        eng.model = _model.Qwen3Model.synthetic(n_layers=n_layers, seed=seed, device=eng.device)
+        eng._init_common()
+        return eng
+
+    def _init_common(self):
+        self.stream = torch.cuda.Stream(device=self.device)   # default priority
+        self.shape = None
+        self.tree_T = int(os.environ.get("ENGINE_TREE_T", "0"))
+        self.prefill_budget_rows = None    # rows per causal prefill chunk (None: 4096)
+        self.tree_stats = None
+
+    # -------------------------------------------------------------- state
+    def _state(self, B, S, N):
+        sh = self.shape
+        if sh is not None and (sh.B, sh.S, sh.N) == (B, S, N):
+            return sh
+        if sh is not None:
+            sh.decode.close()
+        self.shape = None
+        gc.collect()
+        torch.cuda.empty_cache()
+        with torch.cuda.stream(self.stream):
+            sh = _Shape(self.model, self.stream, B, S, N, self.tree_T, self.prefill_budget_rows)
+        self.stream.synchronize()
+        self.shape = sh
+        return sh
+
+    @staticmethod
+    def _check_ids(input_ids, vocab):
+        if not input_ids or not isinstance(input_ids, (list, tuple)):
+            raise ValueError("input_ids must be a non-empty list of token-id lists")
+        S = len(input_ids[0])
+        if S == 0 or any(len(r) != S for r in input_ids):
+            raise ValueError("every sequence in input_ids must have the same, non-zero length")
+        t = torch.tensor(input_ids, dtype=torch.int64)
+        if int(t.min()) < 0 or int(t.max()) >= vocab:
+            raise IndexError(f"token ids must lie in [0, {vocab})")
+        return t
+
+    # -------------------------------------------------------------- API
+    def generate(self, input_ids, max_new_tokens):
+        N = int(max_new_tokens)
+        if N <= 0:
+            return
+        ids = self._check_ids(input_ids, self.model.V)
+        B, S = ids.shape
+        gc_was = gc.isenabled()
+        gc.disable()
+        try:
+            sh = self._state(B, S, N)
+            yield from self._stream_plain(sh, ids, N)
+        finally:
+            if gc_was:
+                gc.enable()
+
+    def _stream_plain(self, sh, ids, N):
+        """Prefill, then N-1 graph replays of the decode step; the host yields step t-1 while
+        the device runs step t (engine.py:719-757)."""
+        S = sh.S
+        with torch.cuda.stream(self.stream):
+            sh.ids_host.copy_(ids)
+            sh.ids.copy_(sh.ids_host, non_blocking=True)
+            sh.run_prefill()
+            sh.kv.pos.fill_(S)
+            sh.host[0].copy_(sh.kv.tok, non_blocking=True)
+            sh.events[0].record(self.stream)
+            if N > 1 and not sh.graph_ready:
+                # the step reads tok/pos from the device; capture once per shape
+                sh.decode.capture()
+                sh.graph_ready = True
+        for t in range(1, N):
+            with torch.cuda.stream(self.stream):
+                sh.decode.replay()
+                sh.host[t].copy_(sh.kv.tok, non_blocking=True)
+                sh.events[t].record(self.stream)
+            sh.events[t - 1].synchronize()
+            yield sh.host[t - 1].tolist()
+        sh.events[N - 1].synchronize()
+        yield sh.host[N - 1].tolist()
+
+    # -------------------------------------------------------------- tree speculation
+    def generate_tree(self, input_ids, max_new_tokens, drafter, T=64):
+        """Exact token-tree speculative decoding (engine.py:830-908): every step verifies a
+        T-node draft tree per sequence in one block forward and emits the longest
+        greedy-matching path.  ``drafter(seq, T) -> _tree.Tree`` supplies the drafts."""
+        N = int(max_new_tokens)
+        if N <= 0:
+            return
+        ids = self._check_ids(input_ids, self.model.V)
+        B, S = ids.shape
+        old_T = self.tree_T
+        self.tree_T = T
+        try:
+            if self.shape is None or self.shape.tree_T != T or (self.shape.B, self.shape.S, self.shape.N) != (B, S, N):
+                self.shape = None
+            sh = self._state(B, S, N)
+        finally:
+            self.tree_T = old_T
+        yield from _tree.stream_tree(self, sh, ids, N, drafter)

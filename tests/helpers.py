@@ -1,0 +1,60 @@
+"""Shared comparison helpers for the parity tests (bf16 ulp distances, margin rule)."""
+
+import os
+import subprocess
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def ensure_oracle_built():
+    lib = os.path.join(ROOT, "oracle", "_build", "libcsynth.so")
+    if not os.path.exists(lib):
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
+
+
+def bf16_ulp(x):
+    """ulp of bf16 at |x| (fp32 tensor); normal range only, floor at 2^-133."""
+    ax = x.abs().clamp(min=2.0 ** -126)
+    return torch.pow(2.0, torch.floor(torch.log2(ax)) - 7)
+
+
+def ulp_diff(a, b):
+    """Elementwise |a - b| in bf16 ulps of max(|a|, |b|)."""
+    a, b = a.float(), b.float()
+    return (a - b).abs() / bf16_ulp(torch.maximum(a.abs(), b.abs()))
+
+
+def assert_ulp(a, b, max_ulp, what="", abs_floor=0.0):
+    """|a - b| <= max_ulp bf16 ulps (or <= abs_floor) everywhere."""
+    a, b = a.float(), b.float()
+    d = (a - b).abs()
+    bad = (d > max_ulp * bf16_ulp(torch.maximum(a.abs(), b.abs()))) & (d > abs_floor)
+    if bad.any():
+        i = int(bad.flatten().nonzero()[0])
+        raise AssertionError(f"{what}: {int(bad.sum())} elements beyond {max_ulp} ulp; first at "
+                             f"{i}: {a.flatten()[i].item()} vs {b.flatten()[i].item()} "
+                             f"(max ulp {ulp_diff(a, b).max().item():.2f})")
+
+
+def margin_rule(tokens, ref_logits, margin=1e-2):
+    """The north-star token rule on teacher-forced reference logits: at every step where the
+    reference's top-2 margin exceeds `margin`, the emitted token must be the reference argmax;
+    elsewhere it must be one of the near-tied tokens.  Returns the violating steps."""
+    bad = []
+    lg = ref_logits.float()
+    top2 = lg.topk(2, dim=-1).values
+    gap = top2[..., 0] - top2[..., 1]
+    best = lg.max(-1).values
+    for idx in np.ndindex(*tokens.shape):
+        t = int(tokens[idx])
+        val = float(lg[idx][t])
+        if float(gap[idx]) > margin:
+            if val != float(best[idx]):
+                bad.append(idx)
+        elif float(best[idx]) - val > margin:
+            bad.append(idx)
+    return bad

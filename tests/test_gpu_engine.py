@@ -1,0 +1,177 @@
+"""GPU end-to-end parity of the Engine (drop-in for engine/engine.py's Engine) against the golden
+transformers run (tests/golden/config1.json) and the CPU oracle.
+
+Token rule (north star): ids identical at every step where the reference top-2 margin exceeds
+1e-2.  The reference logits for a step are taken teacher-forced on the engine's own prefix
+(the judge's replay, QWEN_ENGINE_CONTRACT.md:105-123), so a legitimate near-tie flip is judged
+on what was actually generated."""
+
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import GOLDEN, ensure_oracle_built, margin_rule
+from oracle import qwen3_ref as R
+from oracle import synth
+
+pytestmark = pytest.mark.gpu
+CFG1 = json.load(open(os.path.join(GOLDEN, "config1.json")))
+
+
+def say(msg):
+    print(f"\n[case] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def Engine():
+    from engine import Engine as E
+    return E
+
+
+@pytest.fixture(scope="module")
+def eng4(Engine):
+    say("Engine.synthetic(4 layers, seed 0)")
+    return Engine.synthetic(n_layers=4, seed=0)
+
+
+@pytest.fixture(scope="module")
+def ref4():
+    ensure_oracle_built()
+    return R.Qwen3Ref.from_synth(0, 4)
+
+
+def test_device_weights_match_golden_run(eng4):
+    say("device-generated weights == golden run's weights (sha256)")
+    slots = dict(eng4.model.slots())
+    for name, digest in CFG1["weight_sha256"].items():
+        t = slots[name].contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+        assert hashlib.sha256(t.tobytes()).hexdigest() == digest, name
+
+
+def test_config1_greedy(eng4, ref4):
+    say("config 1: 4 layers, B=1, S=128, N=32")
+    prompt = CFG1["prompt"]
+    steps = list(eng4.generate(prompt, 32))
+    assert len(steps) == 32 and all(len(s) == 1 for s in steps)
+    toks = np.array(steps).T                                     # [B, N]
+    gold = np.array(CFG1["tokens"])
+    first_tie = next((i for i, m in enumerate(CFG1["margins"]) if m <= 1e-2), 32)
+    assert np.array_equal(toks[0, :first_tie], gold[0, :first_tie]), (toks, gold)
+    tl = ref4.teacher_logits(np.array(prompt), toks)
+    bad = margin_rule(toks, tl, margin=1e-2)
+    worst = float((tl.float().max(-1).values - tl.float().gather(-1, torch.as_tensor(toks)[..., None])[..., 0]).max())
+    print(f"config1 tokens {toks[0].tolist()} worst teacher-forced margin {worst:.4f} "
+          f"violations {bad}", flush=True)
+    assert bad == []
+
+
+def test_generate_resets_state_and_is_deterministic(eng4):
+    say("generate x3 with an intervening prompt: identical ids")
+    p1 = synth.prompt_ids(11, 1, 40).tolist()
+    p2 = synth.prompt_ids(12, 1, 40).tolist()
+    a = list(eng4.generate(p1, 12))
+    b = list(eng4.generate(p2, 12))
+    c = list(eng4.generate(p1, 12))
+    assert a == c and a != b
+    assert list(eng4.generate(p1, 0)) == []
+    assert list(eng4.generate(p1, 1)) == a[:1]
+
+
+def test_prefill_chunking_is_invariant(eng4):
+    say("prefill chunk sizes 7 / 64 / whole prompt give identical ids")
+    p = synth.prompt_ids(13, 2, 96).tolist()
+    outs = []
+    for rows in (14, 128, 4096):
+        eng4.prefill_budget_rows = rows
+        eng4.shape = None
+        outs.append(list(eng4.generate(p, 6)))
+    eng4.prefill_budget_rows = None
+    eng4.shape = None
+    assert outs[0] == outs[1] == outs[2]
+
+
+@pytest.fixture(scope="module")
+def eng2(Engine):
+    say("Engine.synthetic(2 layers, seed 1)")
+    return Engine.synthetic(n_layers=2, seed=1)
+
+
+@pytest.fixture(scope="module")
+def ref2():
+    ensure_oracle_built()
+    return R.Qwen3Ref.from_synth(1, 2)
+
+
+@pytest.mark.parametrize("B,S,N", [(2, 33, 8), (5, 40, 6), (32, 64, 6)])
+def test_batched_decode_paths(eng2, ref2, B, S, N):
+    say(f"batched decode B={B} S={S} N={N} (vector path B<=2, MFMA path B>=3)")
+    prompt = synth.prompt_ids(20 + B, B, S)
+    toks = np.array(list(eng2.generate(prompt.tolist(), N))).T
+    tl = ref2.teacher_logits(prompt, toks)
+    bad = margin_rule(toks, tl, margin=1e-2)
+    assert bad == [], bad
+
+
+def test_tree_verification_is_exact(eng2, ref2):
+    say("tree verification B=2 S=48 N=20 T=64 random 4-4-2-2 drafts")
+    from qdecode import tree as tr
+    prompt = synth.prompt_ids(30, 2, 48)
+    plain = np.array(list(eng2.generate(prompt.tolist(), 20))).T
+    # drafts: the true greedy continuation as one branch of each tree, random ids elsewhere
+    rng = np.random.default_rng(0)
+    cont = {b: prompt[b].tolist() + plain[b].tolist() for b in range(2)}
+
+    def drafter(seq, T):
+        t = tr.branching_tree(seq[-1], T, (4, 4, 2, 2), lambda n: rng.integers(0, 151936, size=n))
+        b = next(i for i in range(2) if cont[i][:len(seq)] == list(seq))
+        truth = cont[b][len(seq):len(seq) + 4]
+        t2 = tr.Tree(seq[-1])
+        t2.add_path(truth, T)
+        for i in range(1, len(t.tokens)):
+            if len(t2.tokens) >= T:
+                break
+            if t.parent[i] == 0:
+                t2.add(0, t.tokens[i])
+        t2.pad(T)
+        return t2
+
+    got = np.array(list(eng2.generate_tree(prompt.tolist(), 20, drafter, T=64))).T
+    stats = eng2.tree_stats
+    print(f"tree passes {stats['passes']} accepted {stats['accepted']}", flush=True)
+    assert stats["passes"] < 19                      # the true branch was accepted at least once
+    tl = ref2.teacher_logits(prompt, got)
+    assert margin_rule(got, tl, margin=1e-2) == []
+    if not np.array_equal(got, plain):              # only a genuine near-tie may differ
+        assert margin_rule(plain, ref2.teacher_logits(prompt, plain), margin=1e-2) == []
+
+
+def test_tree_random_drafts_config5_shape(eng2, ref2):
+    say("tree verification with purely random drafts B=4 S=40 N=6")
+    from qdecode import tree as tr
+    prompt = synth.prompt_ids(31, 4, 40)
+    got = np.array(list(eng2.generate_tree(prompt.tolist(), 6, tr.random_tree_drafter(1), T=64))).T
+    tl = ref2.teacher_logits(prompt, got)
+    assert margin_rule(got, tl, margin=1e-2) == []
+
+
+def test_checkpoint_engine_matches_synthetic(Engine, tmp_path):
+    say("Engine(model_path) on a written 1-layer checkpoint == Engine.synthetic")
+    ensure_oracle_built()
+    synth.write_checkpoint(str(tmp_path), seed=5, n_layers=1)
+    a = Engine(str(tmp_path))
+    b = Engine.synthetic(n_layers=1, seed=5)
+    p = synth.prompt_ids(40, 1, 24).tolist()
+    assert list(a.generate(p, 5)) == list(b.generate(p, 5))
+    assert a.model.cfg["rope_theta"] == 5000000.0 and a.model.L == 1
+
+
+def test_invalid_inputs_raise(eng2):
+    say("invalid input ids raise on the host")
+    with pytest.raises(IndexError):
+        list(eng2.generate([[0, 151936]], 2))
+    with pytest.raises(ValueError):
+        list(eng2.generate([[1, 2], [3]], 2))

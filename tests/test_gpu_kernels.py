@@ -1,0 +1,330 @@
+"""GPU parity of each libqdecode kernel against the CPU oracle (oracle/qwen3_ref.py) on seeded
+inputs.  Bars (north star): embedding gather, argmax index, K/V copies and the synthetic
+generator bit-exact; fused layer kernels within 2 bf16 ulp (fp32 accumulate); fp32 logits
+within 2e-2 max-abs."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_ulp
+from oracle import qwen3_ref as R
+from oracle import synth
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+BF = torch.bfloat16
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from qdecode import ops as o
+    return o
+
+
+def say(msg):
+    print(f"\n[case] {msg}", flush=True)
+
+
+def rnd(g, *shape, scale=1.0):
+    return (torch.randn(shape, generator=g) * scale).to(BF)
+
+
+def sync():
+    torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------ generator
+def test_synth_bitexact(ops):
+    for seed, sid, start, n in [(0, 1, 0, 1 << 20), (1, 16 + 16 * 35 + 6, 12345, 100003),
+                                (0, 17, (1 << 31) - 50, 4096)]:
+        say(f"synth seed={seed} stream={sid} start={start} n={n}")
+        out = torch.empty(n, dtype=BF, device=DEV)
+        ops.synth_bf16(out, seed, sid, start, 0.02)
+        sync()
+        got = out.cpu().view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(got, synth.normal_bf16_bits(seed, sid, start, n))
+
+
+# ------------------------------------------------------------------ config 2 layer kernels
+@pytest.mark.parametrize("B", [1, 8, 64])
+def test_embed_gather_bitexact(ops, B):
+    say(f"embed_gather B={B}")
+    g = torch.Generator().manual_seed(B)
+    table = rnd(g, 151936, 2560)
+    ids = torch.randint(0, 151936, (B,), generator=g)
+    ids[0] = 151935
+    out = ops.embed_gather(ids.to(DEV), table.to(DEV))
+    sync()
+    assert torch.equal(out.cpu(), table[ids])
+
+
+def test_embed_gather_out_of_range_row_is_zero(ops):
+    say("embed_gather out-of-range id")
+    table = torch.ones((64, 2560), dtype=BF, device=DEV)
+    ids = torch.tensor([3, 64, -1], dtype=torch.int64, device=DEV)
+    out = ops.embed_gather(ids, table)
+    sync()
+    assert torch.all(out[0] == 1) and torch.all(out[1:] == 0)
+
+
+@pytest.mark.parametrize("B", [1, 8, 64])
+def test_add_rmsnorm(ops, B):
+    say(f"add_rmsnorm B={B}")
+    g = torch.Generator().manual_seed(100 + B)
+    x, r = rnd(g, B, 2560), rnd(g, B, 2560, scale=4.0)
+    w = rnd(g, 2560, scale=0.1) + 1
+    r_out, y = ops.add_rmsnorm(r.to(DEV), w.to(DEV), 1e-6, x=x.to(DEV))
+    sync()
+    r_ref, y_ref = R.add_rmsnorm(x, r, w)
+    assert torch.equal(r_out.cpu(), r_ref)               # bf16(x + r): one rounding, exact
+    assert_ulp(y.cpu(), y_ref, 2, "add_rmsnorm")
+    y2 = ops.rmsnorm(r.to(DEV), w.to(DEV), 1e-6)         # no residual input
+    sync()
+    assert_ulp(y2.cpu(), R.rmsnorm(r, w), 2, "rmsnorm")
+
+
+@pytest.mark.parametrize("B", [1, 8, 64])
+def test_qk_norm_rope_kv_write(ops, B):
+    say(f"qk_norm_rope B={B} positions U[0,8192)")
+    g = torch.Generator().manual_seed(200 + B)
+    Hq, Hkv, cap = 32, 8, 8192
+    qkv = rnd(g, B, (Hq + 2 * Hkv) * 128, scale=2.0)
+    qn, kn = rnd(g, 128, scale=0.2) + 1, rnd(g, 128, scale=0.2) + 1
+    pos = torch.randint(0, cap, (B,), generator=g)
+    cos, sin = R.rope_tables(cap)
+    kc = torch.zeros((B, Hkv, cap, 128), dtype=BF, device=DEV)
+    vc = torch.zeros_like(kc)
+    q_out = torch.empty((B, 1, Hq, 128), dtype=BF, device=DEV)
+    ops.qk_norm_rope(qkv.to(DEV), qn.to(DEV), kn.to(DEV), cos.to(DEV), sin.to(DEV), pos.to(DEV),
+                     ops.POS_ROW, q_out, kc, vc, B, 1, Hq, Hkv, 1e-6)
+    sync()
+    q = qkv[:, :Hq * 128].view(B, 1, Hq, 128)
+    k = qkv[:, Hq * 128:(Hq + Hkv) * 128].view(B, 1, Hkv, 128)
+    v = qkv[:, (Hq + Hkv) * 128:].view(B, Hkv, 128)
+    q_ref, k_ref = R.qk_norm_rope(q, k, qn, kn, cos[pos][:, None], sin[pos][:, None])
+    assert_ulp(q_out.cpu(), q_ref, 2, "q")
+    kcc, vcc = kc.cpu(), vc.cpu()
+    bi = torch.arange(B)
+    assert_ulp(kcc[bi, :, pos], k_ref[:, 0], 2, "k cache")
+    assert torch.equal(vcc[bi, :, pos], v)               # V is copied as is
+    mask = torch.ones((B, cap), dtype=torch.bool)
+    mask[bi, pos] = False
+    assert torch.all(kcc.permute(0, 2, 1, 3)[mask] == 0)  # nothing else written
+
+
+@pytest.mark.parametrize("B", [1, 8, 64])
+def test_swiglu(ops, B):
+    say(f"swiglu B={B}")
+    g = torch.Generator().manual_seed(300 + B)
+    gu = rnd(g, B, 2 * 9728, scale=3.0)
+    out = ops.swiglu(gu.to(DEV))
+    sync()
+    assert_ulp(out.cpu(), R.swiglu(gu[:, :9728], gu[:, 9728:]), 2, "swiglu")
+
+
+# ------------------------------------------------------------------ projections
+def exact_linear(x, w):
+    """fp64 dot products of the bf16 inputs, rounded once to bf16 (and the fp64 values)."""
+    acc = x.double() @ w.double().T
+    return acc.to(torch.float32).to(BF), acc
+
+
+SHAPES = {"qkv": (6144, 2560), "o": (2560, 4096), "gu": (9728, 2560), "down": (2560, 9728)}
+
+
+@pytest.mark.parametrize("B", [1, 2, 3, 16, 32, 64])
+@pytest.mark.parametrize("name", ["qkv", "o", "gu", "down"])
+def test_linear_epilogues(ops, name, B):
+    say(f"linear {name} B={B}")
+    N, K = SHAPES[name]
+    g = torch.Generator().manual_seed(hash((name, B)) % 1000)
+    w = rnd(g, 2 * N if name == "gu" else N, K, scale=0.02)
+    x = rnd(g, B, K)
+    wd, xd = w.to(DEV), x.to(DEV)
+    if name == "qkv":                                    # RMSNorm prologue, plain epilogue
+        nw = rnd(g, K, scale=0.1) + 1
+        out = ops.linear(xd, wd, ops.EPI_NONE, norm_w=nw.to(DEV), eps=1e-6)
+        sync()
+        want, _ = exact_linear(R.rmsnorm(x, nw).float(), w.float())
+        # the normalised input itself may differ by 1 ulp (reduction order), hence 2 ulp + floor
+        assert_ulp(out.cpu(), want, 2, "qkv", abs_floor=2 ** -9)
+    elif name == "gu":                                   # RMSNorm prologue + SwiGLU epilogue
+        nw = rnd(g, K, scale=0.1) + 1
+        out = ops.linear(xd, wd, ops.EPI_SWIGLU, norm_w=nw.to(DEV), eps=1e-6)
+        sync()
+        h = R.rmsnorm(x, nw)
+        gate, _ = exact_linear(h.float(), w[:N].float())
+        up, _ = exact_linear(h.float(), w[N:].float())
+        assert_ulp(out.cpu(), R.swiglu(gate, up), 2, "gate/up swiglu", abs_floor=2 ** -9)
+    else:                                                # residual epilogue, in place
+        res = rnd(g, B, N, scale=2.0)
+        xo = res.to(DEV).clone()
+        ops.linear(xd, wd, ops.EPI_RES, res=xo, out=xo)
+        sync()
+        acc, _ = exact_linear(x.float(), w.float())
+        assert_ulp(xo.cpu(), (res.float() + acc.float()).to(BF), 2, name, abs_floor=2 ** -9)
+
+
+# ------------------------------------------------------------------ LM head + argmax
+@pytest.mark.parametrize("B", [1, 2, 8])
+def test_lm_head_argmax(ops, B):
+    say(f"lm_head_argmax B={B}")
+    g = torch.Generator().manual_seed(400 + B)
+    V, K = 151936, 2560
+    w = rnd(g, V, K, scale=0.02)
+    x = rnd(g, B, K)
+    nw = rnd(g, K, scale=0.1) + 1
+    logits = torch.empty((B, V), dtype=torch.float32, device=DEV)
+    pos = torch.zeros((1,), dtype=torch.int64, device=DEV)
+    tok = ops.lm_head_argmax(x.to(DEV), w.to(DEV), nw.to(DEV), 1e-6, pos=pos, logits=logits)
+    sync()
+    h = R.rmsnorm(x, nw)
+    exact = h.double() @ w.double().T
+    lg = logits.cpu()
+    assert float((lg.double() - exact).abs().max()) <= 2e-2      # north-star logits bar
+    assert float((lg.double() - exact).abs().max()) <= 1e-3      # what fp32 accumulation gives
+    # the index is bit-exact given the kernel's own bf16 logits (lowest index on ties)
+    own = torch.argmax(lg.to(BF).float(), dim=-1)
+    assert torch.equal(tok.cpu(), own)
+    # and it is the oracle's argmax wherever the oracle's top-2 margin exceeds 1e-2
+    ref = R.linear(h, w).float()
+    top2 = ref.topk(2, dim=-1).values
+    for b in range(B):
+        if float(top2[b, 0] - top2[b, 1]) > 1e-2:
+            assert int(tok[b]) == int(torch.argmax(ref[b]))
+    assert int(pos.item()) == 1                                  # position advanced once
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_lm_head_ties_pick_lowest_index(ops, B):
+    say(f"lm_head ties B={B}")
+    V, K = 151936, 2560
+    g = torch.Generator().manual_seed(7)
+    w = rnd(g, V, K, scale=0.001)
+    x = torch.ones((B, K), dtype=BF)
+    nw = torch.ones(K, dtype=BF)
+    # identical maximal rows in different workgroups / tiles: the lowest index must win
+    for n in (150000, 77777, 40001, 151935):
+        w[n] = 0.05
+    tok = ops.lm_head_argmax(x.to(DEV), w.to(DEV), nw.to(DEV), 1e-6)
+    sync()
+    assert tok.cpu().tolist() == [40001] * B
+
+
+# ------------------------------------------------------------------ attention
+def decode_ref(qkv, qn, kn, cos, sin, kcache, vcache, pos):
+    """Oracle: q/k norm + rope at pos, write K/V at pos, attend keys [0, pos]."""
+    B = qkv.shape[0]
+    q = qkv[:, :4096].view(B, 1, 32, 128)
+    k = qkv[:, 4096:5120].view(B, 1, 8, 128)
+    v = qkv[:, 5120:].view(B, 8, 128)
+    qr, kr = R.qk_norm_rope(q, k, qn, kn, cos[pos][None, None].expand(B, 1, 128),
+                            sin[pos][None, None].expand(B, 1, 128))
+    kc, vc = kcache.clone(), vcache.clone()
+    kc[:, :, pos] = kr[:, 0]
+    vc[:, :, pos] = v
+    vis = torch.zeros((1, 1, 1, kc.shape[2]), dtype=torch.bool)
+    vis[..., :pos + 1] = True
+    o = R.attention(qr.transpose(1, 2), kc, vc, vis)
+    return o[:, :, 0], kc, vc
+
+
+@pytest.mark.parametrize("B,cap,pos", [(1, 768, 0), (1, 768, 1), (1, 768, 63), (1, 768, 64),
+                                       (1, 768, 640), (1, 768, 767), (4, 300, 129),
+                                       (32, 2176, 2100)])
+def test_decode_attention(ops, B, cap, pos):
+    say(f"decode_attention B={B} cap={cap} pos={pos}")
+    g = torch.Generator().manual_seed(500 + B + pos)
+    qkv = rnd(g, B, 6144, scale=2.0)
+    qn, kn = rnd(g, 128, scale=0.2) + 1, rnd(g, 128, scale=0.2) + 1
+    cos, sin = R.rope_tables(cap)
+    kcache = rnd(g, B, 8, cap, 128)
+    vcache = rnd(g, B, 8, cap, 128)
+    kcache[:, :, pos:] = 0
+    vcache[:, :, pos:] = 0
+    kd, vd = kcache.to(DEV), vcache.to(DEV)
+    p = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    out = ops.decode_attention(qkv.to(DEV), qn.to(DEV), kn.to(DEV), cos.to(DEV), sin.to(DEV), p,
+                               kd, vd, 32, 8, 1e-6)
+    sync()
+    o_ref, kc_ref, vc_ref = decode_ref(qkv, qn, kn, cos, sin, kcache, vcache, pos)
+    assert torch.equal(vd.cpu(), vc_ref)
+    assert_ulp(kd.cpu(), kc_ref, 2, "k cache")
+    assert_ulp(out.cpu(), o_ref, 2, "attention out", abs_floor=2 ** -10)
+
+
+def test_decode_attention_repeat_is_deterministic(ops):
+    say("decode_attention repeat x3 bit-identical (tickets reset)")
+    g = torch.Generator().manual_seed(9)
+    B, cap, pos = 2, 1024, 900
+    qkv = rnd(g, B, 6144).to(DEV)
+    qn = torch.ones(128, dtype=BF, device=DEV)
+    cos, sin = (t.to(DEV) for t in R.rope_tables(cap))
+    kd = rnd(g, B, 8, cap, 128).to(DEV)
+    vd = rnd(g, B, 8, cap, 128).to(DEV)
+    p = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    ws = ops.workspace(ops._lib.LIB.qd_decode_attn_workspace_bytes(B, 32, 8, cap), DEV)
+    outs = [ops.decode_attention(qkv, qn, qn, cos, sin, p, kd, vd, 32, 8, 1e-6, ws=ws).cpu()
+            for _ in range(3)]
+    sync()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    assert int(ws.view(torch.int32).cpu().max()) < 2 ** 30   # workspace sane
+
+
+@pytest.mark.parametrize("mode", ["tree", "causal"])
+def test_block_attention(ops, mode):
+    say(f"block_attention {mode}")
+    g = torch.Generator().manual_seed(600)
+    B, T, cap = 2, 64 if mode == "tree" else 40, 1200
+    base = torch.tensor([700, 1100], dtype=torch.int64) if mode == "tree" else torch.tensor([0, 333])
+    base = base.clamp(max=cap - T)
+    q = rnd(g, B, T, 32, 128)
+    kc, vc = rnd(g, B, 8, cap, 128), rnd(g, B, 8, cap, 128)
+    if mode == "tree":
+        rng = np.random.default_rng(1)
+        parent = [-1] + [int(rng.integers(0, i)) for i in range(1, T)]
+        anc = []
+        for i in range(T):
+            m, n = 0, i
+            while n >= 0:
+                m |= 1 << n
+                n = parent[n]
+            anc.append(m)
+        anc_t = torch.tensor([[a - (1 << 64) if a >= 1 << 63 else a for a in anc]] * B)
+    out = ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), base.to(DEV),
+                              anc_t.to(DEV) if mode == "tree" else None)
+    sync()
+    for b in range(B):
+        vis = torch.zeros((T, cap), dtype=torch.bool)
+        for t in range(T):
+            vis[t, :base[b]] = True
+            for jj in range(T):
+                ok = ((anc[t] >> jj) & 1) if mode == "tree" else jj <= t
+                if ok:
+                    vis[t, base[b] + jj] = True
+        o = R.attention(q[b:b + 1].transpose(1, 2), kc[b:b + 1], vc[b:b + 1], vis[None, None])
+        assert_ulp(out[b].cpu(), o[0].transpose(0, 1), 2, f"block row {b}", abs_floor=2 ** -10)
+
+
+def test_kv_compact(ops):
+    say("kv_compact")
+    g = torch.Generator().manual_seed(700)
+    L, B, cap, T = 3, 2, 200, 8
+    k = rnd(g, L, B, 8, cap, 128).to(DEV)
+    v = rnd(g, L, B, 8, cap, 128).to(DEV)
+    k0, v0 = k.cpu(), v.cpu()
+    base = torch.tensor([50, 120])
+    src = torch.tensor([[0, 2, 3, 7, 0, 0, 0, 0], [0, 1, 5, 0, 0, 0, 0, 0]], dtype=torch.int32)
+    cnt = torch.tensor([4, 3], dtype=torch.int32)
+    ops.kv_compact(k, v, base.to(DEV), src.to(DEV), cnt.to(DEV))
+    sync()
+    ke, ve = k0.clone(), v0.clone()
+    for b in range(B):
+        for kk in range(1, int(cnt[b])):
+            s = int(src[b, kk])
+            ke[:, b, :, base[b] + kk] = ke[:, b, :, base[b] + s]
+            ve[:, b, :, base[b] + kk] = ve[:, b, :, base[b] + s]
+    assert torch.equal(k.cpu(), ke) and torch.equal(v.cpu(), ve)

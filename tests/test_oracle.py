@@ -1,0 +1,225 @@
+"""CPU: pin the oracle (oracle/) against the golden vectors transformers wrote
+(tests/golden/make_golden.py), closed forms and library routines."""
+
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import GOLDEN, assert_ulp, ensure_oracle_built, margin_rule
+from oracle import qwen3_ref as R
+from oracle import synth
+
+OPS = np.load(os.path.join(GOLDEN, "ops.npz"))
+CFG1 = json.load(open(os.path.join(GOLDEN, "config1.json")))
+
+
+def T(k):
+    return R.bits_to_bf16(OPS[k])
+
+
+@pytest.fixture(scope="module")
+def ref4():
+    ensure_oracle_built()
+    torch.set_num_threads(min(8, os.cpu_count() or 8))
+    return R.Qwen3Ref.from_synth(0, 4)
+
+
+# ------------------------------------------------------------------ generator
+def test_synth_c_matches_numpy():
+    ensure_oracle_built()
+    for seed, sid, start, n in [(0, 17, 0, 1 << 16), (1, 1, 123456789, 4099), (7, 600, (1 << 33) + 5, 777)]:
+        assert np.array_equal(synth.normal_bf16_bits(seed, sid, start, n),
+                              synth.normal_bf16_bits_c(seed, sid, start, n))
+
+
+def test_synth_statistics():
+    v = synth.bf16_bits_to_f32(synth.normal_bf16_bits(3, 99, 0, 1 << 20))
+    assert abs(float(v.mean())) < 1e-4
+    assert abs(float(v.std()) / 0.02 - 1.0) < 0.01
+    assert float(np.abs(v).max()) < 0.02 * 4.95        # Irwin-Hall(8) support: +-4.899 sigma
+
+
+def test_synth_prompt_ids():
+    ids = synth.prompt_ids(0, 2, 4096)
+    assert ids.min() >= 0 and ids.max() < 151936
+    assert np.array_equal(ids[0, :128], np.array(CFG1["prompt"][0]))
+
+
+def test_weight_sha256_matches_golden_run():
+    """The golden transformers run used exactly these generator bits."""
+    ensure_oracle_built()
+    cfg = dict(synth.QWEN3_4B)
+    cfg["num_hidden_layers"] = 4
+    shapes = synth.param_shapes(cfg)
+    for name, digest in CFG1["weight_sha256"].items():
+        bits = synth.param_bits(0, name, shapes[name])
+        assert hashlib.sha256(bits.tobytes()).hexdigest() == digest, name
+
+
+def test_bf16_rounding_is_rne():
+    x = np.array([1.0, 1.00390625, 1.01171875, -2.5e-39, 3.0e38, np.inf, 1 + 2 ** -8, 1 + 3 * 2 ** -8],
+                 dtype=np.float32)
+    got = synth.f32_to_bf16_bits(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ------------------------------------------------------------------ ops vs transformers
+def test_rmsnorm_golden():
+    assert torch.equal(R.rmsnorm(T("rms_x"), T("rms_w")), T("rms_y"))
+    assert torch.equal(R.rmsnorm(T("hrms_x"), T("hrms_w")), T("hrms_y"))
+
+
+def test_rmsnorm_closed_forms():
+    w = T("rms_w")
+    c = torch.full((1, 2560), 0.75, dtype=torch.bfloat16)      # c * rsqrt(c^2 + eps) -> 1.0
+    assert torch.equal(R.rmsnorm(c, w)[0], w)
+    z = torch.zeros((1, 2560), dtype=torch.bfloat16)
+    assert torch.equal(R.rmsnorm(z, w), z)
+    x = T("rms_x")[:1]
+    assert torch.equal(R.rmsnorm(x * 2, w), R.rmsnorm(x, w))   # scale invariance (power of 2)
+
+
+def test_add_rmsnorm_is_residual_then_norm():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn((3, 2560), generator=g).bfloat16()
+    r = torch.randn((3, 2560), generator=g).bfloat16()
+    w = T("rms_w")
+    r2, y = R.add_rmsnorm(x, r, w)
+    assert torch.equal(r2, (x.float() + r.float()).bfloat16())
+    assert torch.equal(y, R.rmsnorm(r2, w))
+
+
+def test_rope_golden():
+    assert np.array_equal(R.rope_inv_freq().numpy(), OPS["rope_inv_freq"])
+    pos = torch.from_numpy(OPS["rope_pos"])
+    cos, sin = R.rope_tables(int(pos.max()) + 1)
+    assert torch.equal(cos[pos], T("rope_cos"))
+    assert torch.equal(sin[pos], T("rope_sin"))
+    pp = torch.from_numpy(OPS["ar_pos"])
+    c, s = cos[pp][None, None], sin[pp][None, None]
+    assert torch.equal(R.apply_rope(T("ar_q"), c, s), T("ar_qo"))
+    assert torch.equal(R.apply_rope(T("ar_k"), c, s), T("ar_ko"))
+
+
+def test_rope_closed_forms():
+    cos, sin = R.rope_tables(3000)
+    assert torch.all(cos[0] == 1) and torch.all(sin[0] == 0)
+    x = T("ar_q")[0, :, 0]                                     # [32, 128]
+    assert torch.equal(R.apply_rope(x, cos[0], sin[0]), x)      # position 0 is the identity
+    # the rotation preserves each (d, d + 64) pair's norm up to the bf16 rounding points
+    y = R.apply_rope(x, cos[2047], sin[2047]).float()
+    xf = x.float()
+    n_in = xf[:, :64] ** 2 + xf[:, 64:] ** 2
+    n_out = y[:, :64] ** 2 + y[:, 64:] ** 2
+    assert torch.allclose(n_out, n_in, rtol=2e-2, atol=1e-3)
+    # frequency 0 has angle = position exactly (inv_freq[0] = 1)
+    assert float(R.rope_inv_freq()[0]) == 1.0
+
+
+def test_swiglu_golden():
+    assert torch.equal(R.swiglu(T("mlp_g"), T("mlp_u")), T("mlp_act"))
+    z = torch.zeros(4, dtype=torch.bfloat16)
+    assert torch.equal(R.swiglu(z, torch.ones(4, dtype=torch.bfloat16)), z)
+
+
+def test_attention_golden():
+    od = R.attention(T("sd_q"), T("sd_k"), T("sd_v"), torch.ones((1, 1, 1, 37), dtype=torch.bool))
+    assert_ulp(od, T("sd_o"), 2, "decode sdpa", abs_floor=2 ** -10)
+    vis = torch.tril(torch.ones((6, 6), dtype=torch.bool))[None, None]
+    oc = R.attention(T("sc_q"), T("sc_k"), T("sc_v"), vis)
+    assert_ulp(oc, T("sc_o"), 2, "causal sdpa", abs_floor=2 ** -10)
+
+
+def test_attention_closed_forms():
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn((1, 8, 1, 128), generator=g).bfloat16()
+    k = torch.randn((1, 2, 5, 128), generator=g).bfloat16()
+    v = torch.randn((1, 2, 5, 128), generator=g).bfloat16()
+    one = torch.zeros((1, 1, 1, 5), dtype=torch.bool)
+    one[..., 3] = True
+    o = R.attention(q, k, v, one)                               # one visible key -> its V
+    assert torch.equal(o, R.repeat_kv(v, 4)[:, :, 3:4])
+    ks = k[:, :, :1].expand(1, 2, 5, 128).contiguous()          # identical keys -> mean(V)
+    o = R.attention(q, ks, v, torch.ones((1, 1, 1, 5), dtype=torch.bool))
+    mean = R.repeat_kv(v, 4).float().mean(2, keepdim=True)
+    assert_ulp(o, mean, 2, "mean of V", abs_floor=2 ** -10)
+    # library check: fp32 math SDPA on the same bf16 inputs (differs only by P's bf16 rounding,
+    # |dP| <= 2^-9 P, so |do| <= 2^-9 max|V|)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q.float(), R.repeat_kv(k, 4).float(), R.repeat_kv(v, 4).float())
+    bound = 2 ** -9 * float(v.float().abs().max()) + 2 ** -12
+    assert_ulp(R.attention(q, k, v, torch.ones((1, 1, 1, 5), dtype=torch.bool)), ref, 2, "sdpa fp32",
+               abs_floor=bound)
+
+
+def test_decoder_layer_golden(ref4):
+    y = ref4.decoder_layer(0, T("layer_x"))
+    assert_ulp(y, T("layer_y"), 2, "decoder layer 0", abs_floor=2 ** -10)
+
+
+# ------------------------------------------------------------------ config 1 end to end
+def test_config1_greedy_against_golden(ref4):
+    prompt = np.array(CFG1["prompt"])
+    gold = np.array(CFG1["tokens"])
+    toks, logits = ref4.greedy(prompt, 32)
+    toks = toks.numpy()
+    margins = CFG1["margins"]
+    # identical ids at every step up to the first golden near-tie (margin <= 1e-2)
+    first_tie = next((i for i, m in enumerate(margins) if m <= 1e-2), len(margins))
+    assert np.array_equal(toks[0, :first_tie], gold[0, :first_tie])
+    # before the first divergence the oracle's top logits sit within 2 bf16 ulp of transformers'
+    div = next((i for i in range(32) if toks[0, i] != gold[0, i]), 32)
+    for s in range(div):
+        tv = logits[s][0].float().topk(8).values
+        assert_ulp(tv, torch.tensor(CFG1["top_values"][s]), 2, f"step {s} top-8")
+    # the golden ids satisfy the margin rule under the oracle's teacher-forced logits
+    tl = ref4.teacher_logits(prompt, gold)
+    assert margin_rule(gold, tl, margin=0.07) == []
+
+
+def test_teacher_force_of_own_greedy_is_zero(ref4):
+    prompt = np.array(CFG1["prompt"])[:, :32]
+    toks, _ = ref4.greedy(prompt, 6)
+    m = ref4.teacher_force(prompt, toks)
+    assert float(m.max()) <= 0.07                          # cached decode vs one full forward
+
+
+# ------------------------------------------------------------------ tree verification oracle
+@pytest.fixture(scope="module")
+def ref1():
+    ensure_oracle_built()
+    return R.Qwen3Ref.from_synth(1, 1)
+
+
+def test_tree_chain_equals_causal(ref1):
+    prompt = synth.prompt_ids(1, 1, 12)
+    chain = synth.prompt_ids(2, 1, 6)
+    cache = ref1.new_cache(1, 32)
+    ref1.prefill(torch.as_tensor(prompt), cache)
+    T_ = chain.shape[1]
+    anc = np.array([[(1 << (t + 1)) - 1 for t in range(T_)]], dtype=np.uint64)
+    lt = ref1.verify_tree(chain, np.arange(T_)[None], anc, [12], cache)
+    c2 = ref1.new_cache(1, 32)
+    full = ref1.prefill(torch.as_tensor(np.concatenate([prompt, chain], 1)), c2, last_only=False)
+    assert torch.equal(lt[0], full[0, 12:])
+
+
+def test_tree_paths_equal_sequential_decode(ref1):
+    prompt = synth.prompt_ids(3, 1, 10)
+    # root + 2 children, each with one child: nodes 0; 1,2 (depth 1); 3 (child of 1), 4 (child of 2)
+    toks = np.array([[11, 22, 33, 44, 55]])
+    depth = np.array([[0, 1, 1, 2, 2]])
+    anc = np.array([[1, 0b11, 0b101, 0b1011, 0b10101]], dtype=np.uint64)
+    cache = ref1.new_cache(1, 32)
+    ref1.prefill(torch.as_tensor(prompt), cache)
+    lt = ref1.verify_tree(toks, depth, anc, [10], cache)
+    for node, path in [(3, [11, 22, 44]), (4, [11, 33, 55]), (2, [11, 33])]:
+        c2 = ref1.new_cache(1, 32)
+        seq = np.concatenate([prompt, np.array([path])], 1)
+        full = ref1.prefill(torch.as_tensor(seq), c2, last_only=True)
+        assert torch.equal(lt[0, node], full[0, -1]), node
