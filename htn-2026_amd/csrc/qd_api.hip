@@ -32,11 +32,14 @@ struct AttnWs {
   float* ml;
   int* tickets;
 };
+// Tickets are carved before any size-dependent region, so a workspace reused with other
+// shapes (a shorter prefill chunk, fewer rows) still finds its zeroed tickets at the same
+// offsets; every other region is fully written before it is read on each call.
 AttnWs carve_decode_attn(Carver& c, int64_t B, int64_t Hq, int64_t Hkv, int64_t splits) {
   AttnWs a;
+  a.tickets = c.take<int>(B * Hkv);
   a.acc = c.take<float>(B * Hq * splits * 128);
   a.ml = c.take<float>(B * Hq * splits * 2);
-  a.tickets = c.take<int>(B * Hkv);
   return a;
 }
 
@@ -51,9 +54,9 @@ LmWs carve_lm(Carver& c, int64_t rows, int64_t V, int64_t K) {
   LmWs l;
   const bool vec = gemv_supported(rows, K) && K == 2560;
   l.parts = vec ? lm_vec_parts(V) : gemm_argmax_parts(V);
+  l.ticket = c.take<int>(1);
   l.val = c.take<float>(rows * l.parts);
   l.idx = c.take<int32_t>(rows * l.parts);
-  l.ticket = c.take<int>(1);
   l.xn = vec ? nullptr : c.take<bf16_t>(rows * K);
   return l;
 }
@@ -358,12 +361,15 @@ int qd_decode_step(const qd_weights* w, const qd_decode_state* st, void* stream)
 // ------------------------------------------------------------------ block (tree / prefill chunk)
 int64_t qd_block_workspace_bytes(const qd_weights* w, int64_t batch, int64_t T, int64_t cap) {
   if (!w || batch <= 0 || T <= 0 || cap <= 0) return 0;
-  const int64_t lm_rows = batch * T;  // upper bound (last_only uses batch rows)
+  // LM region first (its ticket at offset 0), sized for either row count (all or last rows)
+  Carver a(nullptr), b(nullptr);
+  carve_lm(a, batch, w->vocab, w->hidden);
+  carve_lm(b, batch * T, w->vocab, w->hidden);
   Carver c(nullptr);
+  c.off = a.off > b.off ? a.off : b.off;
   const int64_t rows = batch * T * w->n_q_heads * block_attn_splits(cap);
   c.take<float>(rows * 128);
   c.take<float>(rows * 2);
-  carve_lm(c, lm_rows, w->vocab, w->hidden);
   return c.off;
 }
 
@@ -372,8 +378,9 @@ int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
   const int64_t B = st->batch, T = st->T, cap = st->cap, H = w->hidden, I = w->inter, V = w->vocab;
   const int Hq = w->n_q_heads, Hkv = w->n_kv_heads;
   if (B <= 0 || T <= 0 || cap <= 0 || !st->k_cache || !st->v_cache || !st->cos || !st->sin ||
-      !st->tokens || !st->base || !st->out_tok || !st->x || !st->xn || !st->qkv || !st->q ||
-      !st->attn || !st->act)
+      !st->tokens || !st->base || !st->x || !st->xn || !st->qkv || !st->q || !st->attn ||
+      !st->act || st->lm_mode < QD_LM_ALL || st->lm_mode > QD_LM_NONE ||
+      (st->lm_mode != QD_LM_NONE && !st->out_tok))
     return QD_EARG;
   if (!st->causal && (!st->anc || !st->depth || T > 64)) return QD_EARG;
   if (!st->workspace || st->workspace_bytes < qd_block_workspace_bytes(w, B, T, cap)) return QD_EWS;
@@ -381,11 +388,11 @@ int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
   const int64_t M = B * T;
   const int64_t splits = block_attn_splits(cap);
   Carver c(st->workspace);
+  const int64_t lm_rows = st->lm_mode == QD_LM_ALL ? M : B;
+  LmWs lw = carve_lm(c, lm_rows, V, H);  // ticket at offset 0 whatever T is
   const int64_t arows = M * Hq * splits;
   float* acc = c.take<float>(arows * 128);
   float* ml = c.take<float>(arows * 2);
-  const int64_t lm_rows = st->last_only ? B : M;
-  LmWs lw = carve_lm(c, lm_rows, V, H);
   const int64_t NQKV = qkv_width(w), QD = (int64_t)Hq * 128;
   const int64_t layer_kv = B * Hkv * cap * 128;
 
@@ -412,7 +419,8 @@ int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
     launch_gemm(st->act, I, M, w->w_down + l * H * I, H, I, st->x, H, st->x, H, EPI_RES, nullptr,
                 nullptr, nullptr, s);
   }
-  if (st->last_only)
+  if (st->lm_mode == QD_LM_NONE) return launched();
+  if (st->lm_mode == QD_LM_LAST)
     return lm_head(st->x + (T - 1) * H, T * H, w->embed, V, H, B, w->final_norm, w->eps,
                    st->out_tok, nullptr, nullptr, lw, s);
   return lm_head(st->x, H, w->embed, V, H, M, w->final_norm, w->eps, st->out_tok, nullptr, nullptr,

@@ -23,6 +23,7 @@ import torch
 
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 
+from qdecode import _lib  # noqa: E402
 from qdecode import model as _model  # noqa: E402
 from qdecode import tree as _tree  # noqa: E402
 
@@ -38,9 +39,10 @@ class _Shape:
         self.kv = _model.KVState(model, B, cap)
         self.stream = stream
         self.chunk = _model.prefill_chunk(B, S, prefill_rows or 4096)
-        self.prefill = _model.BlockRunner(self.kv, stream, self.chunk, causal=True, last_only=True)
+        self.prefill = _model.BlockRunner(self.kv, stream, self.chunk, causal=True,
+                                           lm_mode=_lib.LM_LAST)
         self.decode = _model.DecodeRunner(self.kv, stream)
-        self.tree = (_model.BlockRunner(self.kv, stream, tree_T, causal=False, last_only=False)
+        self.tree = (_model.BlockRunner(self.kv, stream, tree_T, causal=False, lm_mode=_lib.LM_ALL)
                      if tree_T else None)
         self.ids = torch.zeros((B, S), dtype=torch.int64, device=model.device)
         self.ids_host = torch.empty((B, S), dtype=torch.int64, pin_memory=True)
@@ -57,7 +59,8 @@ class _Shape:
             # the block step reads tokens as [B, T] contiguous
             pr.tokens.view(-1)[:B * T].view(B, T).copy_(self.ids[:, c0:c0 + T])
             pr.base.fill_(c0)
-            pr.enqueue(T)
+            # only the chunk holding the last prompt token needs the LM head
+            pr.enqueue(T, lm_mode=_lib.LM_LAST if c0 + T == S else _lib.LM_NONE)
         self.kv.tok.copy_(pr.out_tok)
 
 

@@ -14,6 +14,7 @@ LIB_PATH = os.environ.get("QDECODE_LIB", os.path.join(HERE, "libqdecode.so"))
 QD_EARG, QD_EWS, QD_ESTATE = -1, -2, -3
 EPI_NONE, EPI_RES, EPI_SWIGLU = 0, 1, 2
 POS_T, POS_SHARED, POS_ROW, POS_TREE = 0, 1, 2, 3
+LM_ALL, LM_LAST, LM_NONE = 0, 1, 2
 
 p, i32, i64, u64, f32 = C.c_void_p, C.c_int32, C.c_int64, C.c_uint64, C.c_float
 
@@ -45,7 +46,7 @@ class DecodeState(C.Structure):
 
 class BlockState(C.Structure):
     """qd_block_state (include/qdecode.h)."""
-    _fields_ = [("batch", i32), ("T", i32), ("causal", i32), ("last_only", i32), ("cap", i64),
+    _fields_ = [("batch", i32), ("T", i32), ("causal", i32), ("lm_mode", i32), ("cap", i64),
                 ("k_cache", p), ("v_cache", p), ("cos", p), ("sin", p), ("tokens", p),
                 ("base", p), ("depth", p), ("anc", p), ("c_base", p), ("c_src", p),
                 ("c_cnt", p), ("out_tok", p), ("x", p), ("xn", p), ("qkv", p), ("q", p),

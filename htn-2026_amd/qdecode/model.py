@@ -219,10 +219,10 @@ class BlockRunner:
     """T_max tokens per sequence through every layer (qd_block_step): causal prompt chunks
     (prefill) or tree verification with ancestor masks."""
 
-    def __init__(self, kv, stream, t_max, causal, last_only):
+    def __init__(self, kv, stream, t_max, causal, lm_mode):
         m = kv.model
         self.kv, self.model, self.stream = kv, m, stream
-        self.t_max, self.causal, self.last_only = t_max, causal, last_only
+        self.t_max, self.causal, self.lm_mode = t_max, causal, lm_mode
         B, dev = kv.B, m.device
         M = B * t_max
         e = lambda *s: torch.empty(s, dtype=BF16, device=dev)  # noqa: E731
@@ -236,15 +236,15 @@ class BlockRunner:
         self.depth = z(B, t_max)
         self.anc = z(B, t_max)                     # uint64 masks stored in int64
         self.c_base, self.c_src, self.c_cnt = z(B), z(B, t_max, dt=torch.int32), z(B, dt=torch.int32)
-        self.out_tok = z(B if last_only else M)
+        self.out_tok = z(M if lm_mode == _lib.LM_ALL else B)
         nbytes = _lib.LIB.qd_block_workspace_bytes(C.byref(m.qd), B, t_max, kv.cap)
         self.ws = torch.zeros((nbytes,), dtype=torch.uint8, device=dev)
         self.graph = None
 
-    def state(self, T, compact=False):
+    def state(self, T, compact=False, lm_mode=None):
         kv = self.kv
         return _lib.BlockState(
-            kv.B, T, 1 if self.causal else 0, 1 if self.last_only else 0, kv.cap,
+            kv.B, T, 1 if self.causal else 0, self.lm_mode if lm_mode is None else lm_mode, kv.cap,
             kv.k.data_ptr(), kv.v.data_ptr(), kv.cos.data_ptr(), kv.sin.data_ptr(),
             self.tokens.data_ptr(), self.base.data_ptr(),
             None if self.causal else self.depth.data_ptr(),
@@ -254,11 +254,11 @@ class BlockRunner:
             self.x.data_ptr(), self.xn.data_ptr(), self.qkv.data_ptr(), self.q.data_ptr(),
             self.attn.data_ptr(), self.act.data_ptr(), self.ws.data_ptr(), self.ws.numel())
 
-    def enqueue(self, T=None, compact=False):
+    def enqueue(self, T=None, compact=False, lm_mode=None):
         T = self.t_max if T is None else T
         if not 0 < T <= self.t_max:
             raise ValueError(f"T={T} outside (0, {self.t_max}]")
-        st = self.state(T, compact)
+        st = self.state(T, compact, lm_mode)
         _lib.call("qd_block_step", C.byref(self.model.qd), C.byref(st), self.stream.cuda_stream)
 
 

@@ -171,12 +171,17 @@ typedef struct {
 int64_t qd_decode_workspace_bytes(const qd_weights *w, int64_t batch, int64_t cap);
 int qd_decode_step(const qd_weights *w, const qd_decode_state *st, void *stream);
 
+#define QD_LM_ALL 0
+#define QD_LM_LAST 1
+#define QD_LM_NONE 2
+
 /* One forward of T tokens per sequence through all layers (tree verification, or a causal
  * chunk of the prompt), writing their K/V and the greedy token after each row. */
 typedef struct {
   int32_t batch, T;
   int32_t causal;           /* 1: token t sees block slots <= t (prefill chunk); 0: anc mask */
-  int32_t last_only;        /* 1: LM head only on token T-1 of each row (out_tok [batch]) */
+  int32_t lm_mode;          /* QD_LM_ALL: every row (out_tok [batch*T]); QD_LM_LAST: token T-1
+                               of each row (out_tok [batch]); QD_LM_NONE: K/V only */
   int64_t cap;
   uint16_t *k_cache, *v_cache;   /* [L, batch, Hkv, cap, 128] */
   const uint16_t *cos, *sin;     /* [cap, 128] */
@@ -187,7 +192,7 @@ typedef struct {
   const int64_t *c_base;         /* optional KV compaction before the forward (NULL: none) */
   const int32_t *c_src;          /* [batch * T] */
   const int32_t *c_cnt;          /* [batch] */
-  int64_t *out_tok;              /* [batch * T] or [batch] with last_only */
+  int64_t *out_tok;              /* see lm_mode (may be NULL with QD_LM_NONE) */
   uint16_t *x;                   /* [batch * T, hidden] */
   uint16_t *xn;                  /* [batch * T, hidden] */
   uint16_t *qkv;                 /* [batch * T, (Hq + 2 Hkv) * 128] */

@@ -40,10 +40,18 @@ def assert_ulp(a, b, max_ulp, what="", abs_floor=0.0):
                              f"(max ulp {ulp_diff(a, b).max().item():.2f})")
 
 
+# Cross-implementation noise floor for the oracle-side token rule: the oracle (torch CPU,
+# oneDNN accumulation order) and transformers' own run already disagree by up to 2 bf16 ulp of
+# the top logit (tests/test_oracle.py: the golden ids sit up to 0.0625 below the oracle's
+# argmax), so against the oracle a "near tie" is a top-2 gap within 2 ulp at |logit| < 8.
+ORACLE_TIE = 0.0625 + 1e-6
+
+
 def margin_rule(tokens, ref_logits, margin=1e-2):
     """The north-star token rule on teacher-forced reference logits: at every step where the
     reference's top-2 margin exceeds `margin`, the emitted token must be the reference argmax;
-    elsewhere it must be one of the near-tied tokens.  Returns the violating steps."""
+    elsewhere it must be one of the near-tied tokens.  Returns the violating steps as
+    (index, top-2 gap, emitted token's deficit)."""
     bad = []
     lg = ref_logits.float()
     top2 = lg.topk(2, dim=-1).values
@@ -52,9 +60,10 @@ def margin_rule(tokens, ref_logits, margin=1e-2):
     for idx in np.ndindex(*tokens.shape):
         t = int(tokens[idx])
         val = float(lg[idx][t])
+        deficit = float(best[idx]) - val
         if float(gap[idx]) > margin:
-            if val != float(best[idx]):
-                bad.append(idx)
-        elif float(best[idx]) - val > margin:
-            bad.append(idx)
+            if deficit != 0:
+                bad.append((idx, float(gap[idx]), deficit))
+        elif deficit > margin:
+            bad.append((idx, float(gap[idx]), deficit))
     return bad

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_ulp
+from helpers import assert_ulp, bf16_ulp
 from oracle import qwen3_ref as R
 from oracle import synth
 
@@ -165,7 +165,13 @@ def test_linear_epilogues(ops, name, B):
         ops.linear(xd, wd, ops.EPI_RES, res=xo, out=xo)
         sync()
         acc, _ = exact_linear(x.float(), w.float())
-        assert_ulp(xo.cpu(), (res.float() + acc.float()).to(BF), 2, name, abs_floor=2 ** -9)
+        want = (res.float() + acc.float()).to(BF)
+        # bf16(res + bf16(acc)): one ulp of bf16(acc) may survive cancellation into the sum,
+        # so the bound is ulp(acc) + 2 ulp(out)
+        d = (xo.cpu().float() - want.float()).abs()
+        bound = bf16_ulp(acc.float()) + 2 * bf16_ulp(torch.maximum(xo.cpu().float().abs(),
+                                                                   want.float().abs()))
+        assert bool((d <= bound).all()), f"{name}: max excess {float((d - bound).max())}"
 
 
 # ------------------------------------------------------------------ LM head + argmax
@@ -215,6 +221,16 @@ def test_lm_head_ties_pick_lowest_index(ops, B):
 
 
 # ------------------------------------------------------------------ attention
+def p_round_bound(v, qkv=None):
+    """Attention outputs differ from the oracle by where P is rounded to bf16: online softmax
+    rounds exp(s - m_running), the oracle exp(s - m_global); each term moves by at most one
+    bf16 rounding (2^-9 relative) on either side, so |do| <= 2^-8 max|V| (+ a 2^-12 floor)."""
+    m = float(v.float().abs().max())
+    if qkv is not None:
+        m = max(m, float(qkv[:, 5120:].float().abs().max()))
+    return 2 ** -8 * m + 2 ** -12
+
+
 def decode_ref(qkv, qn, kn, cos, sin, kcache, vcache, pos):
     """Oracle: q/k norm + rope at pos, write K/V at pos, attend keys [0, pos]."""
     B = qkv.shape[0]
@@ -253,7 +269,7 @@ def test_decode_attention(ops, B, cap, pos):
     o_ref, kc_ref, vc_ref = decode_ref(qkv, qn, kn, cos, sin, kcache, vcache, pos)
     assert torch.equal(vd.cpu(), vc_ref)
     assert_ulp(kd.cpu(), kc_ref, 2, "k cache")
-    assert_ulp(out.cpu(), o_ref, 2, "attention out", abs_floor=2 ** -10)
+    assert_ulp(out.cpu(), o_ref, 2, "attention out", abs_floor=p_round_bound(vcache, qkv))
 
 
 def test_decode_attention_repeat_is_deterministic(ops):
@@ -270,8 +286,8 @@ def test_decode_attention_repeat_is_deterministic(ops):
     outs = [ops.decode_attention(qkv, qn, qn, cos, sin, p, kd, vd, 32, 8, 1e-6, ws=ws).cpu()
             for _ in range(3)]
     sync()
+    # a ticket that was not reset would leave the merge undone and the fresh output garbage
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
-    assert int(ws.view(torch.int32).cpu().max()) < 2 ** 30   # workspace sane
 
 
 @pytest.mark.parametrize("mode", ["tree", "causal"])
@@ -306,7 +322,8 @@ def test_block_attention(ops, mode):
                 if ok:
                     vis[t, base[b] + jj] = True
         o = R.attention(q[b:b + 1].transpose(1, 2), kc[b:b + 1], vc[b:b + 1], vis[None, None])
-        assert_ulp(out[b].cpu(), o[0].transpose(0, 1), 2, f"block row {b}", abs_floor=2 ** -10)
+        assert_ulp(out[b].cpu(), o[0].transpose(0, 1), 2, f"block row {b}",
+                   abs_floor=p_round_bound(vc))
 
 
 def test_kv_compact(ops):
