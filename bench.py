@@ -1,0 +1,238 @@
+"""Decode benchmark on one MI355X: Qwen3-4B-shaped bf16 greedy decode through the HIP engine.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-b32] [--no-cpu]
+
+Workloads:
+  value  config 3 -- 36 layers, B=1, prompt 512, up to 256 new tokens: decode tok/s over K timed
+         steps (one step = one hipGraph replay of the whole decode step: embed, 36 layers,
+         LM head + argmax), after W warm-up steps; inputs resident in HBM.
+  b32    config 4 -- 36 layers, B=32, prompts of 2048, up to 128 new tokens (same method).
+Weights are seeded random-init N(0, 0.02) generated on the device; prompt ids uniform.
+
+Roofline: the dominant kernel (gate/up GEMV + SwiGLU) is timed live with HIP events on the
+engine's stream, as a hipGraph of its 36 per-layer launches (each on its own layer's weights,
+so nothing is cache resident) replayed R times; achieved = algorithmic bytes per launch / mean
+launch time.  ``step_roofline`` does the same for the whole step: weights + KV read per step /
+step time.  cpu_baseline times the CPU oracle (oracle/qwen3_ref.py, same architecture and
+generator) on this host's cores on a bounded sample.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "htn-2026_amd"))
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "decode tok/s (Qwen3-4B bf16, B=1 & B=32) + achieved HBM GB/s vs peak"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def decode_run(eng, B, S, N, warmup, steps, seed):
+    """Prefill once, W untimed decode steps, then exactly K timed steps (graph replays)."""
+    import numpy as np
+    import torch
+    K = min(steps, N - 1 - warmup)
+    if K <= 0:
+        raise ValueError(f"steps + warmup must be < {N}")
+    rng = np.random.default_rng(seed)
+    ids = torch.as_tensor(rng.integers(0, eng.model.V, size=(B, S)), dtype=torch.int64)
+    sh = eng._state(B, S, N)
+    st = eng.stream
+    t0 = time.perf_counter()
+    with torch.cuda.stream(st):
+        sh.ids.copy_(ids)
+        sh.run_prefill()
+        sh.kv.pos.fill_(S)
+        if not sh.graph_ready:
+            sh.decode.capture()
+            sh.graph_ready = True
+    st.synchronize()
+    prefill_s = time.perf_counter() - t0
+    with torch.cuda.stream(st):
+        for _ in range(warmup):
+            sh.decode.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    with torch.cuda.stream(st):
+        e0.record(st)
+        for _ in range(K):
+            sh.decode.replay()
+        e1.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    ms = e0.elapsed_time(e1) / K
+    ctx_mean = S + warmup + (K - 1) / 2.0 + 1           # keys read per step, averaged
+    kv_bytes = B * ctx_mean * eng.model.kv_bytes_per_token
+    step_bytes = eng.model.weight_bytes + kv_bytes
+    return sh, {"B": B, "S": S, "K": K, "ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / K,
+                "tok_s": B * 1e3 / ms, "prefill_s": prefill_s, "bytes_per_step": step_bytes,
+                "achieved_gbs": step_bytes / (ms * 1e-3) / 1e9}
+
+
+def time_gu_kernel(eng, sh, reps=20):
+    """Mean duration of the gate/up GEMV + SwiGLU launch (B rows) over all layers' weights."""
+    import ctypes as C
+
+    import torch
+    from qdecode import _lib, ops
+    m, st, dec = eng.model, eng.stream, sh.decode
+    with torch.cuda.stream(st):
+        _lib.call("qd_graph_begin", st.cuda_stream)
+        try:
+            for l in range(m.L):
+                ops.linear(dec.x, m.w_gu[l], ops.EPI_SWIGLU, norm_w=m.ln2[l], eps=m.eps, out=dec.act)
+        finally:
+            ex = C.c_void_p()
+            rc = _lib.LIB.qd_graph_end(st.cuda_stream, C.byref(ex))
+        if rc != 0:
+            raise _lib.QDError("qd_graph_end", rc)
+        for _ in range(2):
+            _lib.call("qd_graph_launch", ex, st.cuda_stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(st):
+        e0.record(st)
+        for _ in range(reps):
+            _lib.call("qd_graph_launch", ex, st.cuda_stream)
+        e1.record(st)
+    torch.cuda.synchronize()
+    _lib.LIB.qd_graph_destroy(ex)
+    us = e0.elapsed_time(e1) * 1e3 / (reps * m.L)
+    B = sh.B
+    nbytes = 2 * (2 * m.I * m.H + B * m.H + m.H + B * m.I)   # W_gate|W_up + x + norm w + act
+    return us, nbytes
+
+
+def cpu_baseline(budget_s=15.0, prompt_len=32):
+    """The CPU oracle (torch CPU, oneDNN bf16) on the same 36-layer architecture and
+    generator: prefill a short prompt, then time greedy decode steps for ~budget_s."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, ROOT)
+    from oracle import qwen3_ref, synth
+    lib = os.path.join(ROOT, "oracle", "_build", "libcsynth.so")
+    if not os.path.exists(lib):
+        import subprocess
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
+    threads = torch.get_num_threads()
+    t0 = time.perf_counter()
+    ref = qwen3_ref.Qwen3Ref.from_synth(1, 36)
+    gen_s = time.perf_counter() - t0
+    prompt = torch.as_tensor(synth.prompt_ids(1, 1, prompt_len))
+    cap = prompt_len + 64
+    cache = ref.new_cache(1, cap)
+    with torch.inference_mode():
+        lg = ref.prefill(prompt, cache)
+        tok = qwen3_ref.argmax_lowest(lg[:, -1])
+        n, t1 = 0, time.perf_counter()
+        while n < 3 or (time.perf_counter() - t1 < budget_s and n < 60):
+            lg = ref.decode(tok, prompt_len + n, cache)
+            tok = qwen3_ref.argmax_lowest(lg)
+            n += 1
+        dt = time.perf_counter() - t1
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except Exception:
+        pass
+    return {"value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle/qwen3_ref.py greedy decode, 36-layer Qwen3-4B shape, B=1, "
+                       f"{n} steps after a {prompt_len}-token prefill ({dt:.1f} s; weight "
+                       f"generation {gen_s:.1f} s untimed); torch {torch.__version__} CPU on "
+                       f"{threads} threads of {cpu}")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--b32-steps", type=int, default=100)
+    ap.add_argument("--no-b32", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build is single-GPU (the decode path shards by "
+              "sequence across GPUs with no collective; see DESIGN.md). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from engine import Engine
+
+    torch.cuda.set_device(0)
+    t0 = time.perf_counter()
+    eng = Engine.synthetic(n_layers=36, seed=1)
+    log(f"weights generated on device in {time.perf_counter() - t0:.1f}s "
+        f"({eng.model.weight_bytes / 1e9:.3f} GB per step)")
+
+    sh, r1 = decode_run(eng, B=1, S=512, N=256, warmup=a.warmup, steps=a.steps, seed=3)
+    log(f"B=1: {r1['ms_per_step']:.4f} ms/step, {r1['tok_s']:.1f} tok/s, "
+        f"{r1['achieved_gbs']:.0f} GB/s, prefill {r1['prefill_s']:.2f}s")
+    us, gu_bytes = time_gu_kernel(eng, sh)
+    log(f"gate/up GEMV: {us:.2f} us/launch, {gu_bytes / (us * 1e-6) / 1e9:.0f} GB/s")
+
+    b32 = None
+    if not a.no_b32:
+        eng.shape = None
+        sh = None
+        torch.cuda.empty_cache()
+        sh32, r32 = decode_run(eng, B=32, S=2048, N=128, warmup=10, steps=a.b32_steps, seed=4)
+        log(f"B=32: {r32['ms_per_step']:.4f} ms/step, {r32['tok_s']:.1f} tok/s, "
+            f"{r32['achieved_gbs']:.0f} GB/s, prefill {r32['prefill_s']:.2f}s")
+        b32 = {"workload": "config 4: 36 layers, B=32, prompts 2048, N=128", "steps": r32["K"],
+               "warmup": 10, "ms_per_step": round(r32["ms_per_step"], 5),
+               "value": round(r32["tok_s"], 2), "unit": "tok/s",
+               "step_roofline": {"bound": "hbm", "achieved": round(r32["achieved_gbs"], 1),
+                                 "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                 "frac": round(r32["achieved_gbs"] / PEAK_HBM_GBS, 4),
+                                 "bytes_per_step": int(r32["bytes_per_step"])},
+               "prefill_s": round(r32["prefill_s"], 3)}
+        eng.shape = None
+        del sh32
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not a.no_cpu:
+        eng = None
+        torch.cuda.empty_cache()
+        cpu = cpu_baseline(a.cpu_budget)
+        log(f"cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} threads")
+
+    gu_gbs = gu_bytes / (us * 1e-6) / 1e9
+    line = {
+        "metric": METRIC, "value": round(r1["tok_s"], 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": r1["K"], "warmup": a.warmup, "ms_per_step": round(r1["ms_per_step"], 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded random-init bf16 weights N(0, 0.02) (norm weights 1), "
+                "uniform prompt ids",
+        "config": {"workload": "config 3: Qwen3-4B-shaped 36 layers, B=1, prompt 512, "
+                               "N=256 greedy decode (steps timed after prefill)",
+                   "batch": 1, "prompt_len": 512, "new_tokens": 256, "layers": 36},
+        "roofline": {"bound": "hbm", "kernel": "gemv gate/up + SwiGLU (B=1)",
+                     "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "bytes_per_launch": gu_bytes, "us_per_launch": round(us, 3)},
+        "step_roofline": {"bound": "hbm", "achieved": round(r1["achieved_gbs"], 1),
+                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                          "frac": round(r1["achieved_gbs"] / PEAK_HBM_GBS, 4),
+                          "bytes_per_step": int(r1["bytes_per_step"])},
+        "wall_ms_per_step": round(r1["wall_ms_per_step"], 5),
+        "prefill_s": round(r1["prefill_s"], 3),
+        "b32": b32,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

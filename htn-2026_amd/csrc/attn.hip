@@ -5,7 +5,7 @@
 //              decode_attn.py:26-119): q-RMSNorm + RoPE of the group's 4 q heads, the split that
 //              owns `pos` normalises + ropes the new K, writes K/V into the cache and attends the
 //              new key from LDS; every split runs an online softmax over its cached keys
-//              [start, min(end, pos)); the split that takes the last ticket merges (LSE).
+//              [start, min(end, pos)) and writes (m, l, acc); a second launch merges (LSE).
 // block_attn   T query tokens per sequence (tree verification / chunked prefill, tree.py:72-142):
 //              keys < base[b] are visible to every token, block slot base + j is visible to
 //              token t iff bit j of anc[b, t] (tree) or j <= t (causal chunk).
@@ -127,18 +127,17 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
     const bf16_t* __restrict__ kn, const bf16_t* __restrict__ cos_t,
     const bf16_t* __restrict__ sin_t, const int64_t* __restrict__ pos_ptr, bf16_t* k_cache,
     bf16_t* v_cache, int Hq, int Hkv, int64_t cap, int64_t chunk, float eps, float scale,
-    float* ws_acc, float* ws_ml, int* tickets, bf16_t* out) {
+    float* ws_acc, float* ws_ml) {
   __shared__ float qs[GRP][128];
   __shared__ float knew[128], vnew[128];
   __shared__ float wm[4][GRP], wl[4][GRP];
   __shared__ float wacc[4][GRP][128];
-  __shared__ int last_flag;
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int splits = gridDim.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t pos = pos_ptr[0];
-  if (pos < 0 || pos >= cap) return;  // uniform over the grid: no slot to write, no ticket taken
+  if (pos < 0 || pos >= cap) return;  // uniform over the grid: no slot to write
   const bf16_t* row = qkv + b * qkv_stride;
   const bf16_t* cos_row = cos_t + pos * 128;
   const bf16_t* sin_row = sin_t + pos * 128;
@@ -235,27 +234,29 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
     ws_acc[idx * 128 + d + 1] = A1;
     if ((tid & 63) == 0) { ws_ml[idx * 2] = M; ws_ml[idx * 2 + 1] = L; }
   }
-  int* tk = tickets + b * Hkv + kvh;
-  if (!take_last_ticket(tk, splits, &last_flag)) return;
-  {
-    const int h = tid >> 6, d = (tid & 63) * 2;
-    const int64_t prow = (b * Hq + kvh * GRP + h) * splits;
-    float M = NEG_INF;
-    for (int sp = 0; sp < splits; ++sp) M = fmaxf(M, __builtin_nontemporal_load(ws_ml + (prow + sp) * 2));
-    float num0 = 0.f, num1 = 0.f, den = 0.f;
-    for (int sp = 0; sp < splits; ++sp) {
-      const float ms = __builtin_nontemporal_load(ws_ml + (prow + sp) * 2);
-      if (ms == NEG_INF) continue;
-      const float a = expf(ms - M);
-      den += a * __builtin_nontemporal_load(ws_ml + (prow + sp) * 2 + 1);
-      num0 += a * __builtin_nontemporal_load(ws_acc + (prow + sp) * 128 + d);
-      num1 += a * __builtin_nontemporal_load(ws_acc + (prow + sp) * 128 + d + 1);
-    }
-    bf16_t* o = out + (b * Hq + kvh * GRP + h) * 128;
-    o[d] = (bf16_t)f2bf(num0 / den);
-    o[d + 1] = (bf16_t)f2bf(num1 / den);
+}
+
+// One wave per (token row, head): log-sum-exp merge of the split partials -> bf16 out
+// [rows, Hq*128] (decode_attn.py:74-86, tree.py:130-142).  A separate launch: the kernel
+// boundary is the only cross-workgroup synchronisation, so no workgroup fences or waits.
+__global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict__ ws_acc,
+                                                         const float* __restrict__ ws_ml,
+                                                         int splits, bf16_t* __restrict__ out) {
+  const int64_t r = blockIdx.x;  // (b*T + t)*Hq + h
+  const int d = threadIdx.x * 2;
+  float M = NEG_INF;
+  for (int sp = 0; sp < splits; ++sp) M = fmaxf(M, ws_ml[(r * splits + sp) * 2]);
+  float n0 = 0.f, n1 = 0.f, den = 0.f;
+  for (int sp = 0; sp < splits; ++sp) {
+    const float ms = ws_ml[(r * splits + sp) * 2];
+    if (ms == NEG_INF) continue;
+    const float a = expf(ms - M);
+    den += a * ws_ml[(r * splits + sp) * 2 + 1];
+    n0 += a * ws_acc[(r * splits + sp) * 128 + d];
+    n1 += a * ws_acc[(r * splits + sp) * 128 + d + 1];
   }
-  reset_ticket(tk);
+  out[r * 128 + d] = (bf16_t)f2bf(n0 / den);
+  out[r * 128 + d + 1] = (bf16_t)f2bf(n1 / den);
 }
 
 int64_t decode_attn_splits(int64_t B, int Hkv, int64_t cap) {
@@ -275,12 +276,13 @@ int64_t decode_attn_chunk(int64_t cap, int64_t splits) {
 void launch_decode_attn(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn, const bf16_t* kn,
                         const bf16_t* cos_t, const bf16_t* sin_t, const int64_t* pos,
                         bf16_t* k_cache, bf16_t* v_cache, int64_t B, int Hq, int Hkv, int64_t cap,
-                        int64_t splits, float eps, float* ws_acc, float* ws_ml, int* tickets,
-                        bf16_t* out, hipStream_t s) {
+                        int64_t splits, float eps, float* ws_acc, float* ws_ml, bf16_t* out,
+                        hipStream_t s) {
   const int64_t chunk = decode_attn_chunk(cap, splits);
   decode_attn_kernel<<<dim3((unsigned)splits, (unsigned)Hkv, (unsigned)B), dim3(256), 0, s>>>(
       qkv, qkv_stride, qn, kn, cos_t, sin_t, pos, k_cache, v_cache, Hq, Hkv, cap, chunk, eps,
-      1.0f / sqrtf(128.0f), ws_acc, ws_ml, tickets, out);
+      1.0f / sqrtf(128.0f), ws_acc, ws_ml);
+  attn_merge_kernel<<<dim3((unsigned)(B * Hq)), dim3(64), 0, s>>>(ws_acc, ws_ml, (int)splits, out);
 }
 
 // ------------------------------------------------------------------ block (tree / causal chunk)
@@ -346,27 +348,6 @@ __global__ __launch_bounds__(256) void block_attn_kernel(
   }
 }
 
-// one wave per (token, head): LSE merge of the splits -> out [B*T, Hq*128]
-__global__ __launch_bounds__(64) void block_merge_kernel(const float* __restrict__ ws_acc,
-                                                         const float* __restrict__ ws_ml,
-                                                         int splits, bf16_t* __restrict__ out) {
-  const int64_t r = blockIdx.x;  // (b*T + t)*Hq + h
-  const int d = threadIdx.x * 2;
-  float M = NEG_INF;
-  for (int sp = 0; sp < splits; ++sp) M = fmaxf(M, ws_ml[(r * splits + sp) * 2]);
-  float n0 = 0.f, n1 = 0.f, den = 0.f;
-  for (int sp = 0; sp < splits; ++sp) {
-    const float ms = ws_ml[(r * splits + sp) * 2];
-    if (ms == NEG_INF) continue;
-    const float a = expf(ms - M);
-    den += a * ws_ml[(r * splits + sp) * 2 + 1];
-    n0 += a * ws_acc[(r * splits + sp) * 128 + d];
-    n1 += a * ws_acc[(r * splits + sp) * 128 + d + 1];
-  }
-  out[r * 128 + d] = (bf16_t)f2bf(n0 / den);
-  out[r * 128 + d + 1] = (bf16_t)f2bf(n1 / den);
-}
-
 int64_t block_attn_splits(int64_t cap) { return (cap + BLOCK_CHUNK - 1) / BLOCK_CHUNK; }
 
 void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
@@ -377,6 +358,6 @@ void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_c
   const int64_t TQ = (T + 3) / 4;
   block_attn_kernel<<<dim3((unsigned)splits, (unsigned)Hkv, (unsigned)(B * TQ)), dim3(256), 0, s>>>(
       q, k_cache, v_cache, base, anc, T, Hq, Hkv, cap, 1.0f / sqrtf(128.0f), ws_acc, ws_ml);
-  block_merge_kernel<<<dim3((unsigned)(B * T * Hq)), dim3(64), 0, s>>>(ws_acc, ws_ml, (int)splits,
-                                                                       out);
+  attn_merge_kernel<<<dim3((unsigned)(B * T * Hq)), dim3(64), 0, s>>>(ws_acc, ws_ml, (int)splits,
+                                                                      out);
 }

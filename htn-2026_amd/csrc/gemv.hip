@@ -155,9 +155,9 @@ void launch_gemv(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t N, 
 }
 
 // ------------------------------------------------------------------ LM head + greedy argmax
-// Final RMSNorm prologue, bf16 logits of the tied embedding, per-workgroup (max, lowest index),
-// then the workgroup that takes the last ticket reduces all partials to tok[b] and advances
-// pos (fast.py:380-436; gemv.py:118-154).  RPW rows per wave, double-buffered.
+// Final RMSNorm prologue, bf16 logits of the tied embedding, per-workgroup (max, lowest index)
+// partials; a second launch (argmax_reduce) picks the global (max, lowest index) per row and
+// advances pos (fast.py:380-436; gemv.py:118-154).  RPW rows per wave, double-buffered.
 constexpr int LM_RPW = 8;
 
 int64_t lm_vec_parts(int64_t V) { return (V + 4 * LM_RPW - 1) / (4 * LM_RPW); }
@@ -166,15 +166,12 @@ template <int MB>
 __global__ __launch_bounds__(256) void lm_vec_kernel(const bf16_t* __restrict__ x, int64_t x_stride,
                                                      const bf16_t* __restrict__ w, int V,
                                                      const bf16_t* __restrict__ norm_w, float eps,
-                                                     float* pval, int32_t* pidx, int* ticket,
-                                                     int64_t* tok, int64_t* pos_inc,
-                                                     float* logits) {
+                                                     float* pval, int32_t* pidx, float* logits) {
   constexpr int KCH = 5;  // K = 2560
   extern __shared__ uint4 xs[];
   __shared__ float red[4 * MB];
   __shared__ float wv_best[4][MB];
   __shared__ int32_t wi_best[4][MB];
-  __shared__ int last_flag;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * LM_RPW;
   uint4 buf[2][KCH];
@@ -216,49 +213,19 @@ __global__ __launch_bounds__(256) void lm_vec_kernel(const bf16_t* __restrict__ 
     pval[b * nparts + blockIdx.x] = v;
     pidx[b * nparts + blockIdx.x] = i;
   }
-  if (!take_last_ticket(ticket, (int)nparts, &last_flag)) return;
-  // last workgroup: global (max, lowest index) per row
-  __shared__ float sv[256];
-  __shared__ int32_t si[256];
-  for (int b = 0; b < MB; ++b) {
-    float v = -INFINITY;
-    int32_t i = 0x7FFFFFFF;
-    for (int64_t p = threadIdx.x; p < nparts; p += 256) {
-      const float v2 = __builtin_nontemporal_load(pval + b * nparts + p);
-      const int32_t i2 = __builtin_nontemporal_load(pidx + b * nparts + p);
-      if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
-    }
-    sv[threadIdx.x] = v;
-    si[threadIdx.x] = i;
-    __syncthreads();
-    for (int off = 128; off > 0; off >>= 1) {
-      if (threadIdx.x < off) {
-        const float v2 = sv[threadIdx.x + off];
-        const int32_t i2 = si[threadIdx.x + off];
-        if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 < si[threadIdx.x])) {
-          sv[threadIdx.x] = v2;
-          si[threadIdx.x] = i2;
-        }
-      }
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) tok[b] = si[0] == 0x7FFFFFFF ? 0 : (int64_t)si[0];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0 && pos_inc) pos_inc[0] += 1;
-  reset_ticket(ticket);
 }
 
 void launch_lm_vec(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t V, int64_t K,
                    const bf16_t* norm_w, float eps, int64_t M, float* pval, int32_t* pidx,
-                   int* ticket, int64_t* tok, int64_t* pos_inc, float* logits, hipStream_t s) {
+                   int64_t* tok, int64_t* pos_inc, float* logits, hipStream_t s) {
   (void)K;  // the caller checked K == 2560
   const dim3 grid((unsigned)lm_vec_parts(V)), block(256);
   const size_t lds = (size_t)M * 5 * 64 * sizeof(uint4);
   if (M == 1)
     lm_vec_kernel<1><<<grid, block, lds, s>>>(x, x_stride, w, (int)V, norm_w, eps, pval, pidx,
-                                              ticket, tok, pos_inc, logits);
+                                              logits);
   else
     lm_vec_kernel<2><<<grid, block, lds, s>>>(x, x_stride, w, (int)V, norm_w, eps, pval, pidx,
-                                              ticket, tok, pos_inc, logits);
+                                              logits);
+  launch_argmax_reduce(pval, pidx, lm_vec_parts(V), M, tok, pos_inc, s);
 }

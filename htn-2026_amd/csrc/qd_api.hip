@@ -27,17 +27,15 @@ struct Carver {
   }
 };
 
+// Every workspace region is fully written before it is read within one call: workspaces need
+// no initialisation and may be reused with other shapes.
 struct AttnWs {
   float* acc;
   float* ml;
-  int* tickets;
 };
-// Tickets are carved before any size-dependent region, so a workspace reused with other
-// shapes (a shorter prefill chunk, fewer rows) still finds its zeroed tickets at the same
-// offsets; every other region is fully written before it is read on each call.
 AttnWs carve_decode_attn(Carver& c, int64_t B, int64_t Hq, int64_t Hkv, int64_t splits) {
+  (void)Hkv;
   AttnWs a;
-  a.tickets = c.take<int>(B * Hkv);
   a.acc = c.take<float>(B * Hq * splits * 128);
   a.ml = c.take<float>(B * Hq * splits * 2);
   return a;
@@ -46,7 +44,6 @@ AttnWs carve_decode_attn(Carver& c, int64_t B, int64_t Hq, int64_t Hkv, int64_t 
 struct LmWs {
   float* val;
   int32_t* idx;
-  int* ticket;
   bf16_t* xn;
   int64_t parts;
 };
@@ -54,7 +51,6 @@ LmWs carve_lm(Carver& c, int64_t rows, int64_t V, int64_t K) {
   LmWs l;
   const bool vec = gemv_supported(rows, K) && K == 2560;
   l.parts = vec ? lm_vec_parts(V) : gemm_argmax_parts(V);
-  l.ticket = c.take<int>(1);
   l.val = c.take<float>(rows * l.parts);
   l.idx = c.take<int32_t>(rows * l.parts);
   l.xn = vec ? nullptr : c.take<bf16_t>(rows * K);
@@ -66,8 +62,7 @@ int lm_head(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t V, int64
             int64_t rows, const bf16_t* norm_w, float eps, int64_t* tok, int64_t* pos_inc,
             float* logits, const LmWs& l, hipStream_t s) {
   if (gemv_supported(rows, K) && K == 2560) {
-    launch_lm_vec(x, x_stride, w, V, K, norm_w, eps, rows, l.val, l.idx, l.ticket, tok, pos_inc,
-                  logits, s);
+    launch_lm_vec(x, x_stride, w, V, K, norm_w, eps, rows, l.val, l.idx, tok, pos_inc, logits, s);
   } else {
     launch_add_rmsnorm(nullptr, x, norm_w, nullptr, l.xn, rows, K, x_stride, K, eps, s);
     launch_gemm(l.xn, K, rows, w, V, K, nullptr, 0, nullptr, 0, EPI_ARGMAX, l.val, l.idx, logits, s);
@@ -232,7 +227,7 @@ int qd_decode_attn(const uint16_t* qkv, int64_t qkv_stride, const uint16_t* q_no
   Carver c(workspace);
   AttnWs a = carve_decode_attn(c, batch, n_q_heads, n_kv_heads, splits);
   launch_decode_attn(qkv, qkv_stride, q_norm_w, k_norm_w, cos, sin, pos, k_cache, v_cache, batch,
-                     (int)n_q_heads, (int)n_kv_heads, cap, splits, eps, a.acc, a.ml, a.tickets,
+                     (int)n_q_heads, (int)n_kv_heads, cap, splits, eps, a.acc, a.ml,
                      out, S(stream));
   return launched();
 }
@@ -336,7 +331,7 @@ int qd_decode_step(const qd_weights* w, const qd_decode_state* st, void* stream)
     // attention (q/k norm + RoPE + KV write + split-K + merge)
     launch_decode_attn(st->qkv, NQKV, w->q_norm + l * 128, w->k_norm + l * 128, st->cos, st->sin,
                        st->pos, st->k_cache + l * layer_kv, st->v_cache + l * layer_kv, B, Hq, Hkv,
-                       cap, splits, w->eps, aw.acc, aw.ml, aw.tickets, st->attn, s);
+                       cap, splits, w->eps, aw.acc, aw.ml, st->attn, s);
     // x = x + attn . Wo
     if (vec_q)
       launch_gemv(st->attn, QD, wo, H, QD, st->x, H, st->x, H, nullptr, 0.f, EPI_RES, B, s);
@@ -361,7 +356,7 @@ int qd_decode_step(const qd_weights* w, const qd_decode_state* st, void* stream)
 // ------------------------------------------------------------------ block (tree / prefill chunk)
 int64_t qd_block_workspace_bytes(const qd_weights* w, int64_t batch, int64_t T, int64_t cap) {
   if (!w || batch <= 0 || T <= 0 || cap <= 0) return 0;
-  // LM region first (its ticket at offset 0), sized for either row count (all or last rows)
+  // LM region first, sized for either row count (all rows or the last row per sequence)
   Carver a(nullptr), b(nullptr);
   carve_lm(a, batch, w->vocab, w->hidden);
   carve_lm(b, batch * T, w->vocab, w->hidden);
@@ -389,7 +384,7 @@ int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
   const int64_t splits = block_attn_splits(cap);
   Carver c(st->workspace);
   const int64_t lm_rows = st->lm_mode == QD_LM_ALL ? M : B;
-  LmWs lw = carve_lm(c, lm_rows, V, H);  // ticket at offset 0 whatever T is
+  LmWs lw = carve_lm(c, lm_rows, V, H);
   const int64_t arows = M * Hq * splits;
   float* acc = c.take<float>(arows * 128);
   float* ml = c.take<float>(arows * 2);

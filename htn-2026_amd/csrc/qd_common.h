@@ -63,26 +63,6 @@ __device__ __forceinline__ float rstd_of(float sumsq, int n, float eps) {
   return 1.0f / sqrtf(sumsq / (float)n + eps);
 }
 
-// ---------------------------------------------------------------- cross-workgroup ticket
-// The classic "last block reduces" pattern: every workgroup publishes its partial result,
-// releases it at agent scope and takes a ticket; the workgroup that draws the last ticket
-// acquires and reduces.  No workgroup ever waits on another, so nothing can spin.
-__device__ __forceinline__ bool take_last_ticket(int* ticket, int n_participants, int* lds_flag) {
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int t = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    *lds_flag = (t == n_participants - 1);
-  }
-  __syncthreads();
-  bool last = *lds_flag != 0;
-  if (last) __threadfence();
-  return last;
-}
-__device__ __forceinline__ void reset_ticket(int* ticket) {
-  if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // streaming 128-bit load (weights are read once per step): non-temporal hint
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {

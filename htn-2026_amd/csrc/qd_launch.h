@@ -40,7 +40,7 @@ void launch_gemv(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t N, 
 int64_t lm_vec_parts(int64_t V);
 void launch_lm_vec(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t V, int64_t K,
                    const bf16_t* norm_w, float eps, int64_t M, float* pval, int32_t* pidx,
-                   int* ticket, int64_t* tok, int64_t* pos_inc, float* logits, hipStream_t s);
+                   int64_t* tok, int64_t* pos_inc, float* logits, hipStream_t s);
 
 // gemm.hip (MFMA path, any M)
 int64_t gemm_argmax_parts(int64_t N);
@@ -54,8 +54,8 @@ int64_t decode_attn_chunk(int64_t cap, int64_t splits);
 void launch_decode_attn(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn, const bf16_t* kn,
                         const bf16_t* cos_t, const bf16_t* sin_t, const int64_t* pos,
                         bf16_t* k_cache, bf16_t* v_cache, int64_t B, int Hq, int Hkv, int64_t cap,
-                        int64_t splits, float eps, float* ws_acc, float* ws_ml, int* tickets,
-                        bf16_t* out, hipStream_t s);
+                        int64_t splits, float eps, float* ws_acc, float* ws_ml, bf16_t* out,
+                        hipStream_t s);
 int64_t block_attn_splits(int64_t cap);
 void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
                        const int64_t* base, const uint64_t* anc, int64_t B, int64_t T, int Hq,

@@ -11,10 +11,10 @@
  * QD_EWS (-2) when a workspace is too small; otherwise the hipError_t of the failed launch.
  * No C++ exception crosses this boundary.
  *
- * Workspaces are caller-owned device buffers of the size the matching *_workspace_bytes
- * function returns.  They hold split partials and completion tickets: zero-fill a workspace
- * once after allocating it; every kernel leaves its tickets at zero when it completes.
- * Calls that share one workspace must not run concurrently.
+ * Workspaces are caller-owned device buffers of at least the size the matching
+ * *_workspace_bytes function returns.  They hold split partials that each call writes before
+ * it reads them, so they need no initialisation.  Calls that share one workspace must not run
+ * concurrently (each call is ordered on its stream).
  */
 #ifndef QDECODE_H
 #define QDECODE_H
