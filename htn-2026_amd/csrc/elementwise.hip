@@ -32,6 +32,42 @@ void launch_embed(const int64_t* ids, const bf16_t* table, bf16_t* out, int64_t 
   embed_kernel<<<dim3((unsigned)n), dim3(256), 0, s>>>(ids, table, out, vocab, hidden, out_stride);
 }
 
+// The decode step's first launch also stages the step's RoPE row: every layer's attention then
+// reads it from a fixed address instead of waiting for pos before fetching the table row.
+__global__ __launch_bounds__(256) void embed_rope_kernel(const int64_t* __restrict__ ids,
+                                                         const bf16_t* __restrict__ table,
+                                                         bf16_t* __restrict__ out, int64_t vocab,
+                                                         int64_t hidden, int64_t out_stride,
+                                                         const bf16_t* __restrict__ cos_t,
+                                                         const bf16_t* __restrict__ sin_t,
+                                                         const int64_t* __restrict__ pos,
+                                                         int64_t cap, bf16_t* rope_out) {
+  const int64_t i = blockIdx.x;
+  const int64_t id = ids[i];
+  const bool ok = id >= 0 && id < vocab;
+  const int64_t nch = hidden / 8;
+  const uint4* src = reinterpret_cast<const uint4*>(table + (ok ? id : 0) * hidden);
+  uint4* dst = reinterpret_cast<uint4*>(out + i * out_stride);
+  for (int64_t c = threadIdx.x; c < nch; c += blockDim.x) dst[c] = ok ? src[c] : make_uint4(0, 0, 0, 0);
+  if (i == 0 && threadIdx.x < 256) {
+    const int64_t p = pos[0];
+    if (p >= 0 && p < cap) {
+      const int t = threadIdx.x;
+      rope_out[t] = t < 128 ? cos_t[p * 128 + t] : sin_t[p * 128 + t - 128];
+    }
+  }
+}
+
+void launch_embed_rope(const int64_t* ids, const bf16_t* table, bf16_t* out, int64_t n,
+                       int64_t vocab, int64_t hidden, int64_t out_stride, const bf16_t* cos_t,
+                       const bf16_t* sin_t, const int64_t* pos, int64_t cap, bf16_t* rope_out,
+                       hipStream_t s) {
+  if (n <= 0) return;
+  embed_rope_kernel<<<dim3((unsigned)n), dim3(256), 0, s>>>(ids, table, out, vocab, hidden,
+                                                            out_stride, cos_t, sin_t, pos, cap,
+                                                            rope_out);
+}
+
 // ------------------------------------------------------------------ residual add + RMSNorm
 // r' = bf16(x + r) (x may be null: r' = r), y = bf16(bf16(r' * rstd) * w),
 // rstd = 1 / sqrt(mean(r'^2) + eps) from the bf16-rounded residual (rmsnorm.py:15-32,

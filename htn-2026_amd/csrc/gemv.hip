@@ -17,15 +17,18 @@
 // No split-K: at B <= 2 there are enough rows (2560 .. 151936) to occupy all 256 CUs.
 #include "qd_launch.h"
 
-template <int MB, int KCH>
+// The normalised activation rows go to LDS once per workgroup.  Barriers order LDS only, so
+// the weight loads each wave issued before this prologue stay in flight across it.
+template <int MB, int KCH, int NT>
 __device__ __forceinline__ void stage_x(const bf16_t* __restrict__ x, int64_t x_stride,
                                         const bf16_t* __restrict__ norm_w, float eps, bool norm,
                                         uint4* xs, float* red) {
   constexpr int NCH = KCH * 64;  // 16-byte chunks per row
+  const int nw = NT / 64;
   for (int b = 0; b < MB; ++b) {
     const uint4* xr = reinterpret_cast<const uint4*>(x + b * x_stride);
     float ss = 0.f;
-    for (int c = threadIdx.x; c < NCH; c += 256) {
+    for (int c = threadIdx.x; c < NCH; c += NT) {
       const uint4 v = xr[c];
       xs[b * NCH + c] = v;
       ss += bflo(v.x) * bflo(v.x) + bfhi(v.x) * bfhi(v.x) + bflo(v.y) * bflo(v.y) +
@@ -34,18 +37,16 @@ __device__ __forceinline__ void stage_x(const bf16_t* __restrict__ x, int64_t x_
     }
     if (!norm) continue;
     ss = wave_sum(ss);
-    if ((threadIdx.x & 63) == 0) red[b * 4 + (threadIdx.x >> 6)] = ss;
+    if ((threadIdx.x & 63) == 0) red[b * nw + (threadIdx.x >> 6)] = ss;
   }
-  if (!norm) {
-    __syncthreads();
-    return;
-  }
-  __syncthreads();
+  lds_barrier();
+  if (!norm) return;
   const uint4* wr = reinterpret_cast<const uint4*>(norm_w);
   for (int b = 0; b < MB; ++b) {
-    const float rstd = rstd_of(red[b * 4] + red[b * 4 + 1] + red[b * 4 + 2] + red[b * 4 + 3],
-                               KCH * 512, eps);
-    for (int c = threadIdx.x; c < NCH; c += 256) {
+    float tot = 0.f;
+    for (int q = 0; q < nw; ++q) tot += red[b * nw + q];
+    const float rstd = rstd_of(tot, KCH * 512, eps);
+    for (int c = threadIdx.x; c < NCH; c += NT) {
       const uint4 v = xs[b * NCH + c];
       const uint4 g = wr[c];
       uint4 o;
@@ -56,15 +57,15 @@ __device__ __forceinline__ void stage_x(const bf16_t* __restrict__ x, int64_t x_
       xs[b * NCH + c] = o;
     }
   }
-  __syncthreads();
+  lds_barrier();
 }
 
-template <int KCH>
+template <int KCH, bool STREAM>
 __device__ __forceinline__ void load_row(const bf16_t* __restrict__ w, int64_t n, uint4* dst) {
   const uint4* wr = reinterpret_cast<const uint4*>(w + n * (int64_t)(KCH * 512));
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int j = 0; j < KCH; ++j) dst[j] = ld_stream(wr + lane + 64 * j);
+  for (int j = 0; j < KCH; ++j) dst[j] = STREAM ? ld_stream(wr + lane + 64 * j) : wr[lane + 64 * j];
 }
 
 template <int MB, int KCH>
@@ -79,38 +80,52 @@ __device__ __forceinline__ void dot_row(const uint4* wv, const uint4* xs, float*
   }
 }
 
-template <int MB, int KCH, int EPI, bool NORM>
-__global__ __launch_bounds__(256) void gemv_kernel(const bf16_t* __restrict__ x, int64_t x_stride,
-                                                   const bf16_t* __restrict__ w, int N,
-                                                   bf16_t* out, int64_t out_stride,
-                                                   const bf16_t* res, int64_t res_stride,
-                                                   const bf16_t* __restrict__ norm_w, float eps) {
+// One workgroup = NW waves; wave w owns rows [(blockIdx.x * NW + w) * RPW, ... + RPW).
+// The first row's loads are issued before the LDS prologue, later rows one row ahead.
+template <int MB, int KCH, int EPI, bool NORM, int RPW, int NW, bool STREAM>
+__global__ __launch_bounds__(NW * 64) void gemv_kernel(const bf16_t* __restrict__ x,
+                                                       int64_t x_stride,
+                                                       const bf16_t* __restrict__ w, int N,
+                                                       bf16_t* out, int64_t out_stride,
+                                                       const bf16_t* res, int64_t res_stride,
+                                                       const bf16_t* __restrict__ norm_w,
+                                                       float eps) {
+  constexpr bool SW = EPI == EPI_SWIGLU;
   extern __shared__ uint4 xs[];
-  __shared__ float red[4 * MB];
+  __shared__ float red[NW * MB];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t n = (int64_t)blockIdx.x * 4 + wave;
-  const bool live = n < N;
-  uint4 wg[KCH], wu[EPI == EPI_SWIGLU ? KCH : 1];
-  if (live) {
-    load_row<KCH>(w, n, wg);
-    if constexpr (EPI == EPI_SWIGLU) load_row<KCH>(w, n + N, wu);
+  const int64_t row0 = ((int64_t)blockIdx.x * NW + wave) * RPW;
+  uint4 wa[KCH], ua[SW ? KCH : 1], wb[RPW > 1 ? KCH : 1], ub[(RPW > 1 && SW) ? KCH : 1];
+  if (row0 < N) {
+    load_row<KCH, STREAM>(w, row0, wa);
+    if constexpr (SW) load_row<KCH, STREAM>(w, row0 + N, ua);
   }
-  stage_x<MB, KCH>(x, x_stride, norm_w, eps, NORM, xs, red);
-  if (!live) return;
-  float ag[MB], au[MB];
-  dot_row<MB, KCH>(wg, xs, ag);
-  if constexpr (EPI == EPI_SWIGLU) dot_row<MB, KCH>(wu, xs, au);
-  if (lane < MB) {
-    const int b = lane;
-    float y;
-    if constexpr (EPI == EPI_RES) {
-      y = bf2f(res[b * res_stride + n]) + rbf(ag[b]);
-    } else if constexpr (EPI == EPI_SWIGLU) {
-      y = rbf(silu_f(rbf(ag[b]))) * rbf(au[b]);
-    } else {
-      y = ag[b];
+  stage_x<MB, KCH, NW * 64>(x, x_stride, norm_w, eps, NORM, xs, red);
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t n = row0 + r;
+    if (n >= N) break;
+    uint4* cw = (r & 1) ? wb : wa;
+    uint4* cu = (r & 1) ? ub : ua;
+    if (r + 1 < RPW && n + 1 < N) {
+      load_row<KCH, STREAM>(w, n + 1, (r & 1) ? wa : wb);
+      if constexpr (SW) load_row<KCH, STREAM>(w, n + 1 + N, (r & 1) ? ua : ub);
     }
-    out[b * out_stride + n] = (bf16_t)f2bf(y);
+    float ag[MB], au[MB];
+    dot_row<MB, KCH>(cw, xs, ag);
+    if constexpr (SW) dot_row<MB, KCH>(cu, xs, au);
+    if (lane < MB) {
+      const int b = lane;
+      float y;
+      if constexpr (EPI == EPI_RES) {
+        y = bf2f(res[b * res_stride + n]) + rbf(ag[b]);
+      } else if constexpr (SW) {
+        y = rbf(silu_f(rbf(ag[b]))) * rbf(au[b]);
+      } else {
+        y = ag[b];
+      }
+      out[b * out_stride + n] = (bf16_t)f2bf(y);
+    }
   }
 }
 
@@ -118,14 +133,16 @@ int gemv_supported(int64_t M, int64_t K) {
   return (M >= 1 && M <= 2) && (K == 2560 || K == 4096 || K == 9728);
 }
 
-template <int MB, int KCH>
-static void gemv_dispatch_epi(const bf16_t* x, int64_t xs, const bf16_t* w, int64_t N, bf16_t* out,
-                              int64_t os, const bf16_t* res, int64_t rs, const bf16_t* nw,
-                              float eps, int epi, hipStream_t s) {
-  const dim3 grid((unsigned)((N + 3) / 4)), block(256);
+template <int MB, int KCH, int RPW, int NW, bool STREAM>
+static void gemv_go(const bf16_t* x, int64_t xs, const bf16_t* w, int64_t N, bf16_t* out,
+                    int64_t os, const bf16_t* res, int64_t rs, const bf16_t* nw, float eps,
+                    int epi, hipStream_t s) {
+  const int64_t rows_per_wg = (int64_t)RPW * NW;
+  const dim3 grid((unsigned)((N + rows_per_wg - 1) / rows_per_wg)), block(NW * 64);
   const size_t lds = (size_t)MB * KCH * 64 * sizeof(uint4);
   const bool norm = nw != nullptr;
-#define GO(E, NM) gemv_kernel<MB, KCH, E, NM><<<grid, block, lds, s>>>(x, xs, w, (int)N, out, os, res, rs, nw, eps)
+#define GO(E, NM) \
+  gemv_kernel<MB, KCH, E, NM, RPW, NW, STREAM><<<grid, block, lds, s>>>(x, xs, w, (int)N, out, os, res, rs, nw, eps)
   if (epi == EPI_RES) {
     if (norm) GO(EPI_RES, true); else GO(EPI_RES, false);
   } else if (epi == EPI_SWIGLU) {
@@ -136,13 +153,23 @@ static void gemv_dispatch_epi(const bf16_t* x, int64_t xs, const bf16_t* w, int6
 #undef GO
 }
 
+// Per-shape launch configuration (rows per wave, waves per workgroup, streaming loads), chosen
+// by sweeping rows/wave in {1,2,4} x waves/WG in {4,8,16} x {streaming, plain} loads on MI355X
+// at B = 1 (hipGraph of 36 launches over distinct layers' weights):
+//   qkv 6144x2560 -> 2 rows, 16 waves (7.9 us);  gate/up 2x9728x2560 -> 1 row, 8 waves (17.8 us)
+//   o 2560x4096 -> 1 row, 4 waves (5.8 us);      down 2560x9728 -> 1 row, 4 waves (11.0 us)
 template <int MB>
 static void gemv_dispatch_k(const bf16_t* x, int64_t xs, const bf16_t* w, int64_t N, int64_t K,
                             bf16_t* out, int64_t os, const bf16_t* res, int64_t rs,
                             const bf16_t* nw, float eps, int epi, hipStream_t s) {
-  if (K == 2560) gemv_dispatch_epi<MB, 5>(x, xs, w, N, out, os, res, rs, nw, eps, epi, s);
-  else if (K == 4096) gemv_dispatch_epi<MB, 8>(x, xs, w, N, out, os, res, rs, nw, eps, epi, s);
-  else gemv_dispatch_epi<MB, 19>(x, xs, w, N, out, os, res, rs, nw, eps, epi, s);
+  if (K == 2560) {
+    if (epi == EPI_SWIGLU) gemv_go<MB, 5, 1, 8, true>(x, xs, w, N, out, os, res, rs, nw, eps, epi, s);
+    else gemv_go<MB, 5, 2, 16, true>(x, xs, w, N, out, os, res, rs, nw, eps, epi, s);
+  } else if (K == 4096) {
+    gemv_go<MB, 8, 1, 4, true>(x, xs, w, N, out, os, res, rs, nw, eps, epi, s);
+  } else {
+    gemv_go<MB, 19, 1, 4, true>(x, xs, w, N, out, os, res, rs, nw, eps, epi, s);
+  }
 }
 
 void launch_gemv(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t N, int64_t K,
@@ -175,8 +202,8 @@ __global__ __launch_bounds__(256) void lm_vec_kernel(const bf16_t* __restrict__ 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * LM_RPW;
   uint4 buf[2][KCH];
-  if (row0 < V) load_row<KCH>(w, row0, buf[0]);
-  stage_x<MB, KCH>(x, x_stride, norm_w, eps, true, xs, red);
+  if (row0 < V) load_row<KCH, true>(w, row0, buf[0]);
+  stage_x<MB, KCH, 256>(x, x_stride, norm_w, eps, true, xs, red);
   float bv[MB];
   int32_t bi[MB];
 #pragma unroll
@@ -185,7 +212,7 @@ __global__ __launch_bounds__(256) void lm_vec_kernel(const bf16_t* __restrict__ 
   for (int r = 0; r < LM_RPW; ++r) {
     const int64_t n = row0 + r;
     if (n >= V) break;
-    if (r + 1 < LM_RPW && n + 1 < V) load_row<KCH>(w, n + 1, buf[(r + 1) & 1]);
+    if (r + 1 < LM_RPW && n + 1 < V) load_row<KCH, true>(w, n + 1, buf[(r + 1) & 1]);
     float acc[MB];
     dot_row<MB, KCH>(buf[r & 1], xs, acc);
 #pragma unroll

@@ -228,7 +228,7 @@ int qd_decode_attn(const uint16_t* qkv, int64_t qkv_stride, const uint16_t* q_no
   AttnWs a = carve_decode_attn(c, batch, n_q_heads, n_kv_heads, splits);
   launch_decode_attn(qkv, qkv_stride, q_norm_w, k_norm_w, cos, sin, pos, k_cache, v_cache, batch,
                      (int)n_q_heads, (int)n_kv_heads, cap, splits, eps, a.acc, a.ml,
-                     out, S(stream));
+                     out, false, S(stream));
   return launched();
 }
 
@@ -244,6 +244,7 @@ int qd_block_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_
                   void* workspace, int64_t workspace_bytes, void* stream) {
   if (batch < 0 || T < 0 || n_kv_heads <= 0 || n_q_heads != 4 * n_kv_heads || cap <= 0) return QD_EARG;
   if (anc && T > 64) return QD_EARG;
+  if (block_attn_splits(cap) > 1024) return QD_EARG;  // the merge holds <= 1024 split weights
   if (batch * T == 0) return QD_OK;
   if (!q || !k_cache || !v_cache || !base || !out) return QD_EARG;
   if (!workspace || workspace_bytes < qd_block_attn_workspace_bytes(batch, T, n_q_heads, cap))
@@ -292,6 +293,7 @@ int64_t qd_decode_workspace_bytes(const qd_weights* w, int64_t batch, int64_t ca
   carve_decode_attn(c, batch, w->n_q_heads, w->n_kv_heads, decode_attn_splits(batch, w->n_kv_heads, cap));
   carve_lm(c, batch, w->vocab, w->hidden);
   c.take<bf16_t>(batch * (int64_t)w->hidden);  // normalised activations (MFMA path)
+  c.take<bf16_t>(256);                         // this step's RoPE row
   return c.off;
 }
 
@@ -309,11 +311,12 @@ int qd_decode_step(const qd_weights* w, const qd_decode_state* st, void* stream)
   AttnWs aw = carve_decode_attn(c, B, Hq, Hkv, splits);
   LmWs lw = carve_lm(c, B, V, H);
   bf16_t* xn = c.take<bf16_t>(B * H);
+  bf16_t* rope_row = c.take<bf16_t>(256);
   const int64_t NQKV = qkv_width(w), QD = (int64_t)Hq * 128;
   const int64_t layer_kv = B * Hkv * cap * 128;
   const bool vec_h = gemv_supported(B, H), vec_q = gemv_supported(B, QD), vec_i = gemv_supported(B, I);
 
-  launch_embed(st->tok, w->embed, st->x, B, V, H, H, s);
+  launch_embed_rope(st->tok, w->embed, st->x, B, V, H, H, st->cos, st->sin, st->pos, cap, rope_row, s);
   for (int64_t l = 0; l < w->n_layers; ++l) {
     const bf16_t* wqkv = w->w_qkv + l * NQKV * H;
     const bf16_t* wo = w->w_o + l * H * QD;
@@ -329,9 +332,10 @@ int qd_decode_step(const qd_weights* w, const qd_decode_state* st, void* stream)
       launch_gemm(xn, H, B, wqkv, NQKV, H, st->qkv, NQKV, nullptr, 0, EPI_NONE, nullptr, nullptr, nullptr, s);
     }
     // attention (q/k norm + RoPE + KV write + split-K + merge)
-    launch_decode_attn(st->qkv, NQKV, w->q_norm + l * 128, w->k_norm + l * 128, st->cos, st->sin,
-                       st->pos, st->k_cache + l * layer_kv, st->v_cache + l * layer_kv, B, Hq, Hkv,
-                       cap, splits, w->eps, aw.acc, aw.ml, st->attn, s);
+    launch_decode_attn(st->qkv, NQKV, w->q_norm + l * 128, w->k_norm + l * 128, rope_row,
+                       rope_row + 128, st->pos, st->k_cache + l * layer_kv,
+                       st->v_cache + l * layer_kv, B, Hq, Hkv, cap, splits, w->eps, aw.acc, aw.ml,
+                       st->attn, true, s);
     // x = x + attn . Wo
     if (vec_q)
       launch_gemv(st->attn, QD, wo, H, QD, st->x, H, st->x, H, nullptr, 0.f, EPI_RES, B, s);
@@ -378,6 +382,7 @@ int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
       (st->lm_mode != QD_LM_NONE && !st->out_tok))
     return QD_EARG;
   if (!st->causal && (!st->anc || !st->depth || T > 64)) return QD_EARG;
+  if (block_attn_splits(cap) > 1024) return QD_EARG;
   if (!st->workspace || st->workspace_bytes < qd_block_workspace_bytes(w, B, T, cap)) return QD_EWS;
   hipStream_t s = S(stream);
   const int64_t M = B * T;

@@ -15,20 +15,34 @@ __device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 
 __device__ __forceinline__ float bflo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bfhi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
-// round-to-nearest-even fp32 -> bf16 bits (NaN stays a quiet NaN)
+// round-to-nearest-even fp32 -> bf16 bits: one v_cvt_pk_bf16_f32 (IEEE RNE, NaN stays NaN)
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
-  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  return (uint32_t)__builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 // value rounded through bf16 (the reference materialises this intermediate as a bf16 tensor)
-__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+__device__ __forceinline__ float rbf(float f) { return static_cast<float>(static_cast<__bf16>(f)); }
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 // ---------------------------------------------------------------- wave64 reductions
+// DPP moves within a row of 16 lanes (no LDS crossbar): quad_perm [1,0,3,2], quad_perm
+// [2,3,0,1], row_half_mirror, row_mirror -- after the four adds every lane holds its row's sum.
+#define QD_DPP(v, ctrl) \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, true))
+__device__ __forceinline__ float row16_sum_dpp(float v) {
+  v += QD_DPP(v, 0xB1);
+  v += QD_DPP(v, 0x4E);
+  v += QD_DPP(v, 0x141);
+  v += QD_DPP(v, 0x140);
+  return v;
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  v = row16_sum_dpp(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
   return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
@@ -37,18 +51,20 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 // sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15)
-__device__ __forceinline__ float row16_sum(float v) {
-#pragma unroll
-  for (int m = 8; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
+__device__ __forceinline__ float row16_sum(float v) { return row16_sum_dpp(v); }
 
-// dot of 8 bf16 pairs held in two uint4 (fp32 accumulate, exact products)
+// dot of 8 bf16 pairs held in two uint4, fp32 accumulate: v_dot2_f32_bf16 multiplies two bf16
+// pairs exactly and adds them to the fp32 accumulator (4 VALU ops per 16 bytes instead of
+// unpack + 8 FMAs)
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
 __device__ __forceinline__ float dot8(const uint4 a, const uint4 b, float acc) {
-  acc = fmaf(bflo(a.x), bflo(b.x), acc); acc = fmaf(bfhi(a.x), bfhi(b.x), acc);
-  acc = fmaf(bflo(a.y), bflo(b.y), acc); acc = fmaf(bfhi(a.y), bfhi(b.y), acc);
-  acc = fmaf(bflo(a.z), bflo(b.z), acc); acc = fmaf(bfhi(a.z), bfhi(b.z), acc);
-  acc = fmaf(bflo(a.w), bflo(b.w), acc); acc = fmaf(bfhi(a.w), bfhi(b.w), acc);
+  acc = dot2(a.x, b.x, acc);
+  acc = dot2(a.y, b.y, acc);
+  acc = dot2(a.z, b.z, acc);
+  acc = dot2(a.w, b.w, acc);
   return acc;
 }
 
@@ -62,6 +78,19 @@ __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g));
 __device__ __forceinline__ float rstd_of(float sumsq, int n, float eps) {
   return 1.0f / sqrtf(sumsq / (float)n + eps);
 }
+
+// Workgroup barrier that orders LDS only.  __syncthreads() is a full workgroup fence: it makes
+// the wave wait for every outstanding global load (s_waitcnt vmcnt(0)) before the barrier, which
+// would serialise a kernel's weight stream behind its activation prologue.  LDS visibility needs
+// only lgkmcnt(0).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// plain 128-bit global load
+__device__ __forceinline__ uint4 ld_plain(const uint4* p) { return *p; }
 
 // streaming 128-bit load (weights are read once per step): non-temporal hint
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));

@@ -13,6 +13,11 @@ enum { POS_T = 0, POS_SHARED = 1, POS_ROW = 2, POS_TREE = 3, POS_CHUNK = 4 };
 // elementwise.hip
 void launch_embed(const int64_t* ids, const bf16_t* table, bf16_t* out, int64_t n, int64_t vocab,
                   int64_t hidden, int64_t out_stride, hipStream_t s);
+// embedding gather that also copies this step's RoPE row (cos[pos], sin[pos]) to rope_out[256]
+void launch_embed_rope(const int64_t* ids, const bf16_t* table, bf16_t* out, int64_t n,
+                       int64_t vocab, int64_t hidden, int64_t out_stride, const bf16_t* cos_t,
+                       const bf16_t* sin_t, const int64_t* pos, int64_t cap, bf16_t* rope_out,
+                       hipStream_t s);
 void launch_add_rmsnorm(const bf16_t* x, const bf16_t* res, const bf16_t* w, bf16_t* res_out,
                         bf16_t* y, int64_t rows, int64_t hidden, int64_t in_stride, int64_t y_stride,
                         float eps, hipStream_t s);
@@ -55,7 +60,7 @@ void launch_decode_attn(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn,
                         const bf16_t* cos_t, const bf16_t* sin_t, const int64_t* pos,
                         bf16_t* k_cache, bf16_t* v_cache, int64_t B, int Hq, int Hkv, int64_t cap,
                         int64_t splits, float eps, float* ws_acc, float* ws_ml, bf16_t* out,
-                        hipStream_t s);
+                        bool rope_row, hipStream_t s);
 int64_t block_attn_splits(int64_t cap);
 void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
                        const int64_t* base, const uint64_t* anc, int64_t B, int64_t T, int Hq,
