@@ -27,6 +27,11 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "htn-2026_amd"))
 
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per gate/up launch at B=1, from two rocprofv3 --pmc passes over this script
+# (`--calib-copy-mib 512`): FETCH_SIZE 48,701.0 KiB x 1.99987 + WRITE_SIZE 38.0 KiB x 1.0, the
+# factors being what the same counters read for a 512 MiB device copy.  Summary and commands:
+# profiles/gemv_gate_up_b1_traffic.md.
+GU_TRAFFIC_B1 = 99_771_853
 METRIC = "decode tok/s (Qwen3-4B bf16, B=1 & B=32) + achieved HBM GB/s vs peak"
 
 
@@ -160,6 +165,9 @@ def main():
     ap.add_argument("--no-b32", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="first run one plain device copy of this many MiB: the reference "
+                         "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build is single-GPU (the decode path shards by "
@@ -170,6 +178,15 @@ def main():
     from engine import Engine
 
     torch.cuda.set_device(0)
+    if a.calib_copy_mib > 0:
+        n = a.calib_copy_mib << 19                     # bf16 elements
+        src = torch.ones(n, dtype=torch.bfloat16, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {a.calib_copy_mib} MiB read + {a.calib_copy_mib} MiB written")
+        del src, dst
     t0 = time.perf_counter()
     eng = Engine.synthetic(n_layers=36, seed=1)
     log(f"weights generated on device in {time.perf_counter() - t0:.1f}s "
@@ -220,7 +237,7 @@ def main():
                    "batch": 1, "prompt_len": 512, "new_tokens": 256, "layers": 36},
         "roofline": {"bound": "hbm", "kernel": "gemv gate/up + SwiGLU (B=1)",
                      "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": GU_TRAFFIC_B1,
                      "bytes_per_launch": gu_bytes, "us_per_launch": round(us, 3)},
         "step_roofline": {"bound": "hbm", "achieved": round(r1["achieved_gbs"], 1),
                           "peak": PEAK_HBM_GBS, "unit": "GB/s",
