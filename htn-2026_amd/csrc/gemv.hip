@@ -31,9 +31,7 @@ __device__ __forceinline__ void stage_x(const bf16_t* __restrict__ x, int64_t x_
     for (int c = threadIdx.x; c < NCH; c += NT) {
       const uint4 v = xr[c];
       xs[b * NCH + c] = v;
-      ss += bflo(v.x) * bflo(v.x) + bfhi(v.x) * bfhi(v.x) + bflo(v.y) * bflo(v.y) +
-            bfhi(v.y) * bfhi(v.y) + bflo(v.z) * bflo(v.z) + bfhi(v.z) * bfhi(v.z) +
-            bflo(v.w) * bflo(v.w) + bfhi(v.w) * bfhi(v.w);
+      ss += sumsq8(v);
     }
     if (!norm) continue;
     ss = wave_sum(ss);
@@ -47,14 +45,7 @@ __device__ __forceinline__ void stage_x(const bf16_t* __restrict__ x, int64_t x_
     for (int q = 0; q < nw; ++q) tot += red[b * nw + q];
     const float rstd = rstd_of(tot, KCH * 512, eps);
     for (int c = threadIdx.x; c < NCH; c += NT) {
-      const uint4 v = xs[b * NCH + c];
-      const uint4 g = wr[c];
-      uint4 o;
-      o.x = pack2(norm_elem(bflo(v.x), rstd, bflo(g.x)), norm_elem(bfhi(v.x), rstd, bfhi(g.x)));
-      o.y = pack2(norm_elem(bflo(v.y), rstd, bflo(g.y)), norm_elem(bfhi(v.y), rstd, bfhi(g.y)));
-      o.z = pack2(norm_elem(bflo(v.z), rstd, bflo(g.z)), norm_elem(bfhi(v.z), rstd, bfhi(g.z)));
-      o.w = pack2(norm_elem(bflo(v.w), rstd, bflo(g.w)), norm_elem(bfhi(v.w), rstd, bfhi(g.w)));
-      xs[b * NCH + c] = o;
+      xs[b * NCH + c] = norm8(xs[b * NCH + c], wr[c], rstd);
     }
   }
   lds_barrier();

@@ -1,0 +1,583 @@
+// Persistent decode step for one sequence (B = 1): the whole greedy step -- per layer qkv,
+// attention (+ split merge), o + residual, gate/up + SwiGLU, down + residual, then the final
+// norm, LM head and argmax, pos += 1 -- in ONE launch of one workgroup per CU
+// (engine/kernels/mega.py:1-15 is the reference's persistent tier; arithmetic as its T5 units,
+// fast.py).
+//
+// Why: a B = 1 step is ~216 dependent launches of 2-20 us each; every launch boundary costs a
+// drain, a cache write-back and a ramp-up.  Here each workgroup runs the step's phases in
+// order and, before it waits for a phase's input, issues the loads of that phase's weight rows
+// (which never depend on the input), so HBM keeps streaming weights across phase boundaries.
+//
+// Cross-workgroup hand-off without fences: every produced vector element travels in a 64-bit
+// word {payload (32 bits), tag (32 bits)} written with one agent-scope relaxed atomic store and
+// read with agent-scope relaxed atomic loads (single-copy atomic, coherent across the XCDs'
+// L2s).  A consumer sees either the old word or the whole new one; it waits until the tag
+// equals this launch's tag.  Tags are epoch + 1, where the epoch (a word in the workspace) is
+// read by every workgroup at the start and advanced by workgroup 0 at the very end, after
+// every other workgroup has delivered its LM-head partial (which depends on everything it
+// read).  Every producer region is distinct per layer, so no word is rewritten in a launch.
+// Waits are bounded: after MG_SPIN_LIMIT polls, or once any wait has failed, a wait sets the
+// error word and returns; the launch then completes with garbage instead of hanging, and the
+// host reads the error word (qd_mega_ctl_offset) after the first replay.
+//
+// Every workgroup is resident at once (grid = CU count, one 512-thread workgroup per CU,
+// checked against the occupancy API on the host), phases only wait on earlier phases, and
+// every workgroup runs every phase, so every wait is eventually satisfied.
+//
+// Results are bit-identical to qd_decode_step at B = 1: the GEMV rows use the same per-wave
+// dot order and wave reduction, the RMSNorm statistics the same virtual thread partition
+// (512 threads for the qkv / gate-up prologues, 256 for the final norm), and attention the same
+// units (attn_core.h) with the same split plan.
+#include "qd_launch.h"
+
+#include "attn_core.h"
+
+namespace {
+
+constexpr int MG_NW = 8;                 // waves per workgroup
+constexpr int MG_NT = MG_NW * 64;
+constexpr uint32_t MG_SPIN_LIMIT = 1u << 20;   // polls per wait (~1 s) before giving up
+
+// model shape of this kernel (Qwen3-4B); the host checks the weights against it
+constexpr int H = 2560, INTER = 9728, HQ = 32, HKV = 8, HD = 128;
+constexpr int NQKV = (HQ + 2 * HKV) * HD;     // 6144
+constexpr int MIN_WG = 256;                   // rows per wave below assume >= 256 workgroups
+
+// LL region of one layer (words): the layer's input residual comes from the previous layer's
+// OUT (layer 0 reads the embedding row directly)
+struct Layout {
+  int64_t qkv, att, mid, act, out, part, ml, per_layer, lm;
+};
+
+__host__ __device__ inline Layout ll_layout(int L, int64_t splits) {
+  Layout a;
+  a.qkv = 0;
+  a.att = a.qkv + NQKV / 2;
+  a.mid = a.att + HQ * HD / 2;
+  a.act = a.mid + H / 2;
+  a.out = a.act + INTER / 2;
+  a.part = a.out + H / 2;
+  a.ml = a.part + (splits > 1 ? HQ * splits * HD : 0);
+  a.per_layer = a.ml + (splits > 1 ? HQ * splits * 2 : 0);
+  a.lm = (int64_t)L * a.per_layer;
+  return a;
+}
+
+struct MegaParams {
+  const bf16_t *embed, *final_norm, *w_qkv, *w_o, *w_gu, *w_down, *ln1, *ln2, *q_norm, *k_norm;
+  const bf16_t *cos, *sin;
+  bf16_t *k_cache, *v_cache;
+  int64_t *tok, *pos;
+  bf16_t* x_out;       // final residual [H] (plain stores, for inspection)
+  uint32_t* ctl;       // [0] epoch, [1] error
+  uint64_t* ll;
+  int64_t cap, chunk, vocab;
+  int L, splits;
+  float eps;
+};
+
+// ------------------------------------------------------------------ LL words
+__device__ __forceinline__ void ll_put(uint64_t* p, uint32_t payload, uint32_t tag) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | payload, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ll_raw(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool ll_ready(uint64_t v, uint32_t tag) {
+  return (uint32_t)(v >> 32) == tag;
+}
+
+// Slow path of a wait: poll until the tag arrives; bounded, and a failed wait anywhere makes
+// every later wait give up within 64 polls.
+__device__ __noinline__ uint64_t ll_spin(const uint64_t* p, uint32_t tag, uint32_t* err) {
+  uint64_t v = ll_raw(p);
+  for (uint32_t it = 1; !ll_ready(v, tag); ++it) {
+    if ((it & 63) == 0) {
+      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+      if (it >= MG_SPIN_LIMIT) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+    __builtin_amdgcn_s_sleep(1);
+    v = ll_raw(p);
+  }
+  return v;
+}
+
+__device__ __forceinline__ uint32_t ll_wait(uint64_t v, const uint64_t* p, uint32_t tag,
+                                            uint32_t* err) {
+  if (!ll_ready(v, tag)) v = ll_spin(p, tag, err);
+  return (uint32_t)v;
+}
+
+// words [0, n) of src -> dst (LDS), WPT words per thread, all loads issued before any wait
+template <int WPT>
+__device__ __forceinline__ void ll_fetch_lds(const uint64_t* src, int n, uint32_t tag,
+                                             uint32_t* err, uint32_t* dst) {
+  uint64_t v[WPT];
+#pragma unroll
+  for (int j = 0; j < WPT; ++j) {
+    const int idx = threadIdx.x + j * MG_NT;
+    v[j] = idx < n ? ll_raw(src + idx) : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < WPT; ++j) {
+    const int idx = threadIdx.x + j * MG_NT;
+    if (idx < n) dst[idx] = ll_wait(v[j], src + idx, tag, err);
+  }
+}
+
+// ------------------------------------------------------------------ GEMV pieces
+// lane l reads the 16-byte chunks l, l + 64, ... of a row (as gemv_kernel)
+template <int KCH>
+__device__ __forceinline__ void mg_load_row(const bf16_t* __restrict__ w, int64_t n, uint4* dst) {
+  const uint4* wr = reinterpret_cast<const uint4*>(w + n * (int64_t)(KCH * 512));
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < KCH; ++j) dst[j] = ld_stream(wr + lane + 64 * j);
+}
+
+template <int KCH>
+__device__ __forceinline__ float mg_dot(const uint4* wv, const uint4* xs) {
+  const int lane = threadIdx.x & 63;
+  float a = 0.f;
+#pragma unroll
+  for (int j = 0; j < KCH; ++j) a = dot8(wv[j], xs[lane + 64 * j], a);
+  return wave_sum(a);
+}
+
+// RMSNorm of the raw row in xs (in place), statistics over VNT virtual threads exactly as a
+// VNT-thread workgroup of gemv_kernel / lm_vec_kernel computes them (VNT in {256, 512}).
+template <int KCH, int VNT>
+__device__ __forceinline__ void mg_norm(uint4* xs, const bf16_t* __restrict__ norm_w, float eps,
+                                        float* red) {
+  constexpr int NCH = KCH * 64;
+  static_assert(VNT == 256 || VNT == 512, "virtual thread count");
+  const int tid = threadIdx.x;
+  float ss = 0.f;
+  if (tid < VNT)
+    for (int c = tid; c < NCH; c += VNT) ss += sumsq8(xs[c]);
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0 && tid < VNT) red[tid >> 6] = ss;
+  lds_barrier();
+  float tot = 0.f;
+  for (int q = 0; q < VNT / 64; ++q) tot += red[q];
+  const float rstd = rstd_of(tot, KCH * 512, eps);
+  const uint4* wr = reinterpret_cast<const uint4*>(norm_w);
+  for (int c = tid; c < NCH; c += MG_NT) xs[c] = norm8(xs[c], wr[c], rstd);
+  lds_barrier();
+}
+
+__device__ __forceinline__ void part_range(int64_t n, int p, int P, int64_t& a, int64_t& b) {
+  a = n * p / P;
+  b = n * (p + 1) / P;
+}
+
+struct Smem {
+  uint4 xs[INTER / 8];             // the phase's input row (bf16), up to 9728 values
+  float red[16];
+  uint16_t obuf[64];               // the workgroup's outputs of the phase, in row order
+  float rown[16];                  // residual values of the workgroup's o / down rows
+  float best_v[MG_NW];
+  int32_t best_i[MG_NW];
+  DecodeAttnLds<MG_NW> attn;
+};
+
+// the workgroup's outputs obuf[0, nrows) -> LL words [w0, w0 + nrows / 2) of dst
+__device__ __forceinline__ void put_pairs(Smem& sm, uint64_t* dst, int64_t w0, int nrows,
+                                          uint32_t tag) {
+  const int t = threadIdx.x;
+  if (t < nrows / 2)
+    ll_put(dst + w0 + t, (uint32_t)sm.obuf[2 * t] | ((uint32_t)sm.obuf[2 * t + 1] << 16), tag);
+}
+
+// ------------------------------------------------------------------ phases
+// qkv = RMSNorm(x; ln1) . Wqkv^T   (rows wave, wave + 8, wave + 16 of the workgroup's 24)
+__device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t tag,
+                          int64_t tok) {
+  const int wave = threadIdx.x >> 6;
+  const Layout ly = ll_layout(p.L, p.splits);
+  uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
+  int64_t a, b;
+  part_range(NQKV / 2, wg, P, a, b);
+  const int64_t r0 = 2 * a;
+  const int nr = (int)(2 * (b - a));
+  const bf16_t* W = p.w_qkv + (int64_t)l * NQKV * H;
+  uint4 w[3][5];
+#pragma unroll
+  for (int rr = 0; rr < 3; ++rr)
+    if (wave + rr * MG_NW < nr) mg_load_row<5>(W, r0 + wave + rr * MG_NW, w[rr]);
+  uint32_t* xs32 = reinterpret_cast<uint32_t*>(sm.xs);
+  if (l == 0) {                    // the embedding row (an id outside the vocab reads zeros)
+    const bool ok = tok >= 0 && tok < p.vocab;
+    const uint4* src = reinterpret_cast<const uint4*>(p.embed + (ok ? tok : 0) * H);
+    for (int c = threadIdx.x; c < H / 8; c += MG_NT) sm.xs[c] = ok ? src[c] : make_uint4(0, 0, 0, 0);
+  } else {
+    const uint64_t* prev = p.ll + (int64_t)(l - 1) * ly.per_layer + ly.out;
+    ll_fetch_lds<3>(prev, H / 2, tag, p.ctl + 1, xs32);
+  }
+  lds_barrier();
+  {                                // residual values of this workgroup's o rows
+    int64_t oa, ob;
+    part_range(H / 2, wg, P, oa, ob);
+    const int t = threadIdx.x;
+    if (t < 2 * (ob - oa)) sm.rown[t] = bf2f(reinterpret_cast<const bf16_t*>(sm.xs)[2 * oa + t]);
+  }
+  mg_norm<5, 512>(sm.xs, p.ln1 + (int64_t)l * H, p.eps, sm.red);
+#pragma unroll
+  for (int rr = 0; rr < 3; ++rr) {
+    const int k = wave + rr * MG_NW;
+    if (k < nr) {
+      const float acc = mg_dot<5>(w[rr], sm.xs);
+      if ((threadIdx.x & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(acc);
+    }
+  }
+  lds_barrier();
+  put_pairs(sm, LL + ly.qkv, a, nr, tag);
+}
+
+// one decode-attention unit (KV head, split) of layer l
+__device__ void phase_attn_unit(const MegaParams& p, Smem& sm, int l, int unit, uint32_t tag,
+                                int64_t pos) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const Layout ly = ll_layout(p.L, p.splits);
+  uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
+  const int kvh = unit / p.splits, split = unit % p.splits;
+  const int64_t layer_kv = (int64_t)HKV * p.cap * HD;
+  uint32_t* err = p.ctl + 1;
+  const uint64_t* qkv = LL + ly.qkv;
+  auto fetch = [&](HeadVals& hv) -> int64_t {
+    // element e of the packed qkv row lives in word e / 2, half e & 1; every wave reads a head
+    // row (straight-line code, no wave-divergent branch around a load or wait)
+    const int64_t e = attn_head_elem<MG_NW>(wave, kvh, HQ, HKV);
+    const uint64_t* w1 = qkv + ((e + lane) >> 1);
+    const uint64_t* w2 = qkv + ((e + lane + 64) >> 1);
+    const uint64_t r1 = ll_raw(w1), r2 = ll_raw(w2);
+    const bf16_t* nw = (wave == attn_k_wave<MG_NW>() ? p.k_norm : p.q_norm) + (int64_t)l * HD;
+    hv.w1 = bf2f(nw[lane]); hv.w2 = bf2f(nw[lane + 64]);
+    hv.c1 = bf2f(p.cos[pos * HD + lane]); hv.c2 = bf2f(p.cos[pos * HD + lane + 64]);
+    hv.s1 = bf2f(p.sin[pos * HD + lane]); hv.s2 = bf2f(p.sin[pos * HD + lane + 64]);
+    const uint32_t u1 = ll_wait(r1, w1, tag, err), u2 = ll_wait(r2, w2, tag, err);
+    hv.b1 = (lane & 1) ? u1 >> 16 : u1 & 0xFFFF;
+    hv.b2 = (lane & 1) ? u2 >> 16 : u2 & 0xFFFF;
+    return pos;
+  };
+  auto final_out = [&](int h, int d, float y0, float y1) {
+    ll_put(LL + ly.att + ((int64_t)(kvh * GRP + h) * HD + d) / 2, pack2(y0, y1), tag);
+  };
+  auto partial_out = [&](int h, int d, float A0, float A1, float M, float Lsum) {
+    const int64_t idx = (int64_t)(kvh * GRP + h) * p.splits + split;
+    ll_put(LL + ly.part + idx * HD + d, __float_as_uint(A0), tag);
+    ll_put(LL + ly.part + idx * HD + d + 1, __float_as_uint(A1), tag);
+    if ((threadIdx.x & 63) == 0) {
+      ll_put(LL + ly.ml + idx * 2, __float_as_uint(M), tag);
+      ll_put(LL + ly.ml + idx * 2 + 1, __float_as_uint(Lsum), tag);
+    }
+  };
+  decode_attn_unit<MG_NW>(sm.attn, fetch, final_out, partial_out,
+                          p.k_cache + (int64_t)l * layer_kv, p.v_cache + (int64_t)l * layer_kv,
+                          (int64_t)kvh * p.cap * HD, p.cap, (int64_t)split * p.chunk, p.chunk,
+                          p.splits == 1, p.eps, 1.0f / sqrtf((float)HD));
+}
+
+// LSE merge of q head hq's split partials (one wave) -> ATT words of the head
+__device__ void phase_merge(const MegaParams& p, int l, int hq, uint32_t tag) {
+  const int lane = threadIdx.x & 63;
+  const Layout ly = ll_layout(p.L, p.splits);
+  uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
+  uint32_t* err = p.ctl + 1;
+  const int S = p.splits;
+  const uint64_t* ml = LL + ly.ml + (int64_t)hq * S * 2;
+  const uint64_t* acc = LL + ly.part + (int64_t)hq * S * HD + 2 * lane;
+  const float2 y = merge_splits(
+      S,
+      [&](int sp) {
+        const uint64_t r0 = ll_raw(ml + 2 * sp), r1 = ll_raw(ml + 2 * sp + 1);
+        return make_float2(__uint_as_float(ll_wait(r0, ml + 2 * sp, tag, err)),
+                           __uint_as_float(ll_wait(r1, ml + 2 * sp + 1, tag, err)));
+      },
+      [&](int first, int n, float2 (&a)[MERGE_BATCH]) {
+        uint64_t r[MERGE_BATCH][2];
+#pragma unroll
+        for (int q = 0; q < MERGE_BATCH; ++q)
+          if (q < n) {
+            r[q][0] = ll_raw(acc + (int64_t)(first + q) * HD);
+            r[q][1] = ll_raw(acc + (int64_t)(first + q) * HD + 1);
+          }
+#pragma unroll
+        for (int q = 0; q < MERGE_BATCH; ++q) {
+          if (q < n) {
+            const uint64_t* w0 = acc + (int64_t)(first + q) * HD;
+            a[q] = make_float2(__uint_as_float(ll_wait(r[q][0], w0, tag, err)),
+                               __uint_as_float(ll_wait(r[q][1], w0 + 1, tag, err)));
+          } else {
+            a[q] = make_float2(0.f, 0.f);
+          }
+        }
+      });
+  ll_put(LL + ly.att + (int64_t)hq * (HD / 2) + lane, pack2(y.x, y.y), tag);
+}
+
+// mid = x + bf16(attn . Wo^T)   (10 rows: waves 0..7, waves 0, 1 take a second row)
+__device__ void phase_o(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t tag) {
+  const int wave = threadIdx.x >> 6;
+  const Layout ly = ll_layout(p.L, p.splits);
+  uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
+  int64_t a, b;
+  part_range(H / 2, wg, P, a, b);
+  const int64_t r0 = 2 * a;
+  const int nr = (int)(2 * (b - a));
+  const bf16_t* W = p.w_o + (int64_t)l * H * (HQ * HD);
+  uint4 w[2][8];
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr)
+    if (wave + rr * MG_NW < nr) mg_load_row<8>(W, r0 + wave + rr * MG_NW, w[rr]);
+  ll_fetch_lds<4>(LL + ly.att, HQ * HD / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
+  lds_barrier();
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int k = wave + rr * MG_NW;
+    if (k < nr) {
+      const float acc = mg_dot<8>(w[rr], sm.xs);
+      if ((threadIdx.x & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(sm.rown[k] + rbf(acc));
+    }
+  }
+  lds_barrier();
+  put_pairs(sm, LL + ly.mid, a, nr, tag);
+}
+
+// act = bf16(silu(bf16(g))) * bf16(u), g / u = RMSNorm(mid; ln2) . Wgate / Wup^T
+// (act rows wave + 8 rr of the workgroup's 38; two rows' weights in flight per wave)
+__device__ void phase_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t tag) {
+  const int wave = threadIdx.x >> 6;
+  const Layout ly = ll_layout(p.L, p.splits);
+  uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
+  int64_t a, b;
+  part_range(INTER / 2, wg, P, a, b);
+  const int64_t r0 = 2 * a;
+  const int nr = (int)(2 * (b - a));
+  const bf16_t* W = p.w_gu + (int64_t)l * 2 * INTER * H;
+  constexpr int RW = 5;            // act rows per wave (<= 38 per workgroup)
+  uint4 g[2][5], u[2][5];
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int k = wave + rr * MG_NW;
+    if (k < nr) {
+      mg_load_row<5>(W, r0 + k, g[rr]);
+      mg_load_row<5>(W, r0 + k + INTER, u[rr]);
+    }
+  }
+  ll_fetch_lds<3>(LL + ly.mid, H / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
+  lds_barrier();
+  {                                // residual values of this workgroup's down rows
+    int64_t da, db;
+    part_range(H / 2, wg, P, da, db);
+    const int t = threadIdx.x;
+    if (t < 2 * (db - da)) sm.rown[t] = bf2f(reinterpret_cast<const bf16_t*>(sm.xs)[2 * da + t]);
+  }
+  mg_norm<5, 512>(sm.xs, p.ln2 + (int64_t)l * H, p.eps, sm.red);
+#pragma unroll
+  for (int rr = 0; rr < RW; ++rr) {
+    const int k = wave + rr * MG_NW;
+    if (k < nr) {
+      const float ag = mg_dot<5>(g[rr & 1], sm.xs);
+      const float au = mg_dot<5>(u[rr & 1], sm.xs);
+      const int kn = k + 2 * MG_NW;
+      if (rr + 2 < RW && kn < nr) {
+        mg_load_row<5>(W, r0 + kn, g[rr & 1]);
+        mg_load_row<5>(W, r0 + kn + INTER, u[rr & 1]);
+      }
+      if ((threadIdx.x & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(rbf(silu_f(rbf(ag))) * rbf(au));
+    }
+  }
+  lds_barrier();
+  put_pairs(sm, LL + ly.act, a, nr, tag);
+}
+
+// out = mid + bf16(act . Wdown^T)   (10 rows as phase_o)
+__device__ void phase_down(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t tag) {
+  const int wave = threadIdx.x >> 6;
+  const Layout ly = ll_layout(p.L, p.splits);
+  uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
+  int64_t a, b;
+  part_range(H / 2, wg, P, a, b);
+  const int64_t r0 = 2 * a;
+  const int nr = (int)(2 * (b - a));
+  const bf16_t* W = p.w_down + (int64_t)l * H * INTER;
+  uint4 w[2][19];
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr)
+    if (wave + rr * MG_NW < nr) mg_load_row<19>(W, r0 + wave + rr * MG_NW, w[rr]);
+  ll_fetch_lds<10>(LL + ly.act, INTER / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
+  lds_barrier();
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int k = wave + rr * MG_NW;
+    if (k < nr) {
+      const float acc = mg_dot<19>(w[rr], sm.xs);
+      if ((threadIdx.x & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(sm.rown[k] + rbf(acc));
+    }
+  }
+  lds_barrier();
+  put_pairs(sm, LL + ly.out, a, nr, tag);
+  if (l == p.L - 1 && threadIdx.x < nr) p.x_out[r0 + threadIdx.x] = sm.obuf[threadIdx.x];
+}
+
+// final RMSNorm + LM head over the workgroup's vocab rows: best (bf16 logit, lowest index)
+// -> 2 LL words; four rows in flight per wave
+__device__ void phase_lm(const MegaParams& p, Smem& sm, int wg, int P, uint32_t tag) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const Layout ly = ll_layout(p.L, p.splits);
+  int64_t r0, r1;
+  part_range(p.vocab, wg, P, r0, r1);
+  const int nr = (int)(r1 - r0);
+  uint4 buf[4][5];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    if (wave + s * MG_NW < nr) mg_load_row<5>(p.embed, r0 + wave + s * MG_NW, buf[s]);
+  const uint64_t* last = p.ll + (int64_t)(p.L - 1) * ly.per_layer + ly.out;
+  ll_fetch_lds<3>(last, H / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
+  lds_barrier();
+  mg_norm<5, 256>(sm.xs, p.final_norm, p.eps, sm.red);
+  float bv = -INFINITY;
+  int32_t bi = 0x7FFFFFFF;
+  for (int k0 = wave; k0 < nr; k0 += 4 * MG_NW) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int k = k0 + s * MG_NW;
+      if (k < nr) {
+        const float v = rbf(mg_dot<5>(buf[s], sm.xs));   // the reference's logits are bf16
+        const int kn = k + 4 * MG_NW;
+        if (kn < nr) mg_load_row<5>(p.embed, r0 + kn, buf[s]);
+        if (v > bv) { bv = v; bi = (int32_t)(r0 + k); }  // rows ascend per wave: strict >
+      }
+    }
+  }
+  if (lane == 0) { sm.best_v[wave] = bv; sm.best_i[wave] = bi; }
+  lds_barrier();
+  if (threadIdx.x == 0) {
+    float v = sm.best_v[0];
+    int32_t i = sm.best_i[0];
+    for (int q = 1; q < MG_NW; ++q) {
+      const float v2 = sm.best_v[q];
+      const int32_t i2 = sm.best_i[q];
+      if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+    }
+    ll_put(p.ll + ly.lm + 2 * wg, __float_as_uint(v), tag);
+    ll_put(p.ll + ly.lm + 2 * wg + 1, (uint32_t)i, tag);
+  }
+}
+
+// workgroup 0: global (max, lowest index) over the partials -> tok; pos += 1; epoch += 1
+__device__ void phase_final(const MegaParams& p, Smem& sm, int P, uint32_t tag, uint32_t epoch,
+                            int64_t pos) {
+  const Layout ly = ll_layout(p.L, p.splits);
+  const uint64_t* lm = p.ll + ly.lm;
+  uint32_t* err = p.ctl + 1;
+  float bv = -INFINITY;
+  int32_t bi = 0x7FFFFFFF;
+  for (int q = threadIdx.x; q < P; q += MG_NT) {
+    const uint64_t r0 = ll_raw(lm + 2 * q), r1 = ll_raw(lm + 2 * q + 1);
+    const float v = __uint_as_float(ll_wait(r0, lm + 2 * q, tag, err));
+    const int32_t i = (int32_t)ll_wait(r1, lm + 2 * q + 1, tag, err);
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+  }
+  // wave argmax, then across waves
+  for (int off = 32; off > 0; off >>= 1) {
+    const float v2 = __shfl_xor(bv, off, 64);
+    const int32_t i2 = __shfl_xor(bi, off, 64);
+    if (v2 > bv || (v2 == bv && i2 < bi)) { bv = v2; bi = i2; }
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  lds_barrier();                   // best_v / best_i were read by phase_lm's thread 0
+  if (lane == 0) { sm.best_v[wave] = bv; sm.best_i[wave] = bi; }
+  lds_barrier();
+  if (threadIdx.x == 0) {
+    float v = sm.best_v[0];
+    int32_t i = sm.best_i[0];
+    for (int q = 1; q < MG_NW; ++q) {
+      const float v2 = sm.best_v[q];
+      const int32_t i2 = sm.best_i[q];
+      if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+    }
+    p.tok[0] = i == 0x7FFFFFFF ? 0 : (int64_t)i;
+    p.pos[0] = pos + 1;
+    __hip_atomic_store(p.ctl, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__global__ __launch_bounds__(MG_NT) void mega_step_kernel(MegaParams p) {
+  __shared__ Smem sm;
+  const int wg = blockIdx.x, P = gridDim.x;
+  const int wave = threadIdx.x >> 6;
+  const uint32_t epoch = __hip_atomic_load(p.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t tag = epoch + 1;
+  const int64_t pos = p.pos[0];
+  const int64_t tok = p.tok[0];
+  if (pos < 0 || pos >= p.cap) {   // uniform over the grid: nothing is written, nobody waits
+    if (wg == 0 && threadIdx.x == 0)
+      __hip_atomic_store(p.ctl + 1, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  const int units = HKV * p.splits;
+  const int merge0 = P - HQ;       // workgroups merge0 .. P-1 merge one q head each
+  for (int l = 0; l < p.L; ++l) {
+    phase_qkv(p, sm, l, wg, P, tag, tok);
+    for (int u = wg; u < units; u += P) phase_attn_unit(p, sm, l, u, tag, pos);
+    if (p.splits > 1 && wg >= merge0 && wave == 0) phase_merge(p, l, wg - merge0, tag);
+    phase_o(p, sm, l, wg, P, tag);
+    phase_gu(p, sm, l, wg, P, tag);
+    phase_down(p, sm, l, wg, P, tag);
+  }
+  phase_lm(p, sm, wg, P, tag);
+  if (wg == 0) phase_final(p, sm, P, tag, epoch, pos);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ host side
+int mega_grid() {
+  static int grid = -1;
+  if (grid < 0) {
+    int dev = 0, cus = 0, occ = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, mega_step_kernel, MG_NT, 0) !=
+            hipSuccess) {
+      (void)hipGetLastError();
+      grid = 0;
+    } else {
+      grid = (occ >= 1 && cus >= MIN_WG && cus >= HQ) ? cus : 0;
+    }
+  }
+  return grid;
+}
+
+bool mega_shape_ok(int hidden, int inter, int hq, int hkv, int head_dim) {
+  return hidden == H && inter == INTER && hq == HQ && hkv == HKV && head_dim == HD;
+}
+
+int64_t mega_ll_bytes(int L, int64_t splits, int grid) {
+  const Layout ly = ll_layout(L, splits);
+  return (ly.lm + 2 * (int64_t)grid) * 8;
+}
+
+int64_t mega_splits(int64_t cap) { return decode_attn_splits(1, HKV, cap); }
+
+hipError_t launch_mega_step(const MegaLaunch& m, hipStream_t s) {
+  MegaParams p;
+  p.embed = m.embed; p.final_norm = m.final_norm; p.w_qkv = m.w_qkv; p.w_o = m.w_o;
+  p.w_gu = m.w_gu; p.w_down = m.w_down; p.ln1 = m.ln1; p.ln2 = m.ln2; p.q_norm = m.q_norm;
+  p.k_norm = m.k_norm; p.cos = m.cos; p.sin = m.sin; p.k_cache = m.k_cache;
+  p.v_cache = m.v_cache; p.tok = m.tok; p.pos = m.pos; p.x_out = m.x_out; p.ctl = m.ctl;
+  p.ll = m.ll; p.cap = m.cap; p.vocab = m.vocab; p.L = m.L; p.eps = m.eps;
+  p.splits = (int)mega_splits(m.cap);
+  p.chunk = decode_attn_chunk(m.cap, p.splits);
+  const int grid = mega_grid();
+  if (grid <= 0) return hipErrorInvalidConfiguration;
+  mega_step_kernel<<<dim3((unsigned)grid), dim3(MG_NT), 0, s>>>(p);
+  return hipGetLastError();
+}

@@ -357,6 +357,53 @@ int qd_decode_step(const qd_weights* w, const qd_decode_state* st, void* stream)
   return lm_head(st->x, H, w->embed, V, H, B, w->final_norm, w->eps, st->tok, st->pos, nullptr, lw, s);
 }
 
+// ------------------------------------------------------------------ persistent decode step
+// Workspace: qd_decode_step's region, then (256-byte aligned) the control block {epoch, error}
+// and the hand-off words of the persistent kernel.
+static int64_t mega_ctl_off(const qd_weights* w, int64_t batch, int64_t cap) {
+  return (qd_decode_workspace_bytes(w, batch, cap) + 255) / 256 * 256;
+}
+
+static bool mega_ok(const qd_weights* w, int64_t batch) {
+  return w && batch == 1 && w->hidden % 512 == 0 &&
+         mega_shape_ok(w->hidden, w->inter, w->n_q_heads, w->n_kv_heads, w->head_dim) &&
+         mega_grid() > 0;
+}
+
+int qd_mega_supported(const qd_weights* w, int64_t batch) { return weights_ok(w) && mega_ok(w, batch) ? 1 : 0; }
+
+int64_t qd_mega_workspace_bytes(const qd_weights* w, int64_t batch, int64_t cap) {
+  if (!weights_ok(w) || cap <= 0 || !mega_ok(w, batch)) return 0;
+  return mega_ctl_off(w, batch, cap) + 256 + mega_ll_bytes(w->n_layers, mega_splits(cap), mega_grid());
+}
+
+int64_t qd_mega_ctl_offset(const qd_weights* w, int64_t batch, int64_t cap) {
+  if (!weights_ok(w) || cap <= 0 || !mega_ok(w, batch)) return -1;
+  return mega_ctl_off(w, batch, cap);
+}
+
+int qd_mega_step(const qd_weights* w, const qd_decode_state* st, void* stream) {
+  if (!weights_ok(w) || !st) return QD_EARG;
+  if (!mega_ok(w, st->batch)) return QD_EARG;
+  if (st->cap <= 0 || !st->k_cache || !st->v_cache || !st->cos || !st->sin || !st->tok ||
+      !st->pos || !st->x)
+    return QD_EARG;
+  const int64_t need = qd_mega_workspace_bytes(w, st->batch, st->cap);
+  if (!st->workspace || need <= 0 || st->workspace_bytes < need) return QD_EWS;
+  char* ws = static_cast<char*>(st->workspace);
+  const int64_t off = mega_ctl_off(w, st->batch, st->cap);
+  MegaLaunch m;
+  m.embed = w->embed; m.final_norm = w->final_norm; m.w_qkv = w->w_qkv; m.w_o = w->w_o;
+  m.w_gu = w->w_gu; m.w_down = w->w_down; m.ln1 = w->ln1; m.ln2 = w->ln2;
+  m.q_norm = w->q_norm; m.k_norm = w->k_norm; m.cos = st->cos; m.sin = st->sin;
+  m.k_cache = st->k_cache; m.v_cache = st->v_cache; m.tok = st->tok; m.pos = st->pos;
+  m.x_out = st->x; m.ctl = reinterpret_cast<uint32_t*>(ws + off);
+  m.ll = reinterpret_cast<uint64_t*>(ws + off + 256);
+  m.cap = st->cap; m.vocab = w->vocab; m.L = w->n_layers; m.eps = w->eps;
+  const hipError_t e = launch_mega_step(m, S(stream));
+  return e == hipSuccess ? QD_OK : (int)e;
+}
+
 // ------------------------------------------------------------------ block (tree / prefill chunk)
 int64_t qd_block_workspace_bytes(const qd_weights* w, int64_t batch, int64_t T, int64_t cap) {
   if (!w || batch <= 0 || T <= 0 || cap <= 0) return 0;

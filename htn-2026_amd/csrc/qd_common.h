@@ -71,6 +71,24 @@ __device__ __forceinline__ float dot8(const uint4 a, const uint4 b, float acc) {
 // Qwen3RMSNorm's output element: weight * bf16(x * rstd), rounded to bf16
 __device__ __forceinline__ float norm_elem(float x, float rstd, float w) { return rbf(rbf(x * rstd) * w); }
 
+// sum of squares of 8 packed bf16 values, in one fixed expression order (every RMSNorm
+// prologue uses this, so statistics agree across kernels that partition a row alike)
+__device__ __forceinline__ float sumsq8(const uint4 v) {
+  return bflo(v.x) * bflo(v.x) + bfhi(v.x) * bfhi(v.x) + bflo(v.y) * bflo(v.y) +
+         bfhi(v.y) * bfhi(v.y) + bflo(v.z) * bflo(v.z) + bfhi(v.z) * bfhi(v.z) +
+         bflo(v.w) * bflo(v.w) + bfhi(v.w) * bfhi(v.w);
+}
+
+// y = bf16(bf16(v * rstd) * g) for 8 packed values
+__device__ __forceinline__ uint4 norm8(const uint4 v, const uint4 g, float rstd) {
+  uint4 o;
+  o.x = pack2(norm_elem(bflo(v.x), rstd, bflo(g.x)), norm_elem(bfhi(v.x), rstd, bfhi(g.x)));
+  o.y = pack2(norm_elem(bflo(v.y), rstd, bflo(g.y)), norm_elem(bfhi(v.y), rstd, bfhi(g.y)));
+  o.z = pack2(norm_elem(bflo(v.z), rstd, bflo(g.z)), norm_elem(bfhi(v.z), rstd, bfhi(g.z)));
+  o.w = pack2(norm_elem(bflo(v.w), rstd, bflo(g.w)), norm_elem(bfhi(v.w), rstd, bfhi(g.w)));
+  return o;
+}
+
 // torch silu in fp32 opmath: x / (1 + exp(-x)) (HIP's own expf, IEEE divide)
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 

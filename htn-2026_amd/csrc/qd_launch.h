@@ -55,6 +55,25 @@ void launch_gemm(const bf16_t* x, int64_t x_stride, int64_t M, const bf16_t* w, 
 
 // attn.hip
 int64_t decode_attn_splits(int64_t B, int Hkv, int64_t cap);
+
+// persistent B = 1 decode step (mega.hip)
+struct MegaLaunch {
+  const bf16_t *embed, *final_norm, *w_qkv, *w_o, *w_gu, *w_down, *ln1, *ln2, *q_norm, *k_norm;
+  const bf16_t *cos, *sin;
+  bf16_t *k_cache, *v_cache;
+  int64_t *tok, *pos;
+  bf16_t* x_out;
+  uint32_t* ctl;        // [0] epoch, [1] error; zero before the first launch
+  uint64_t* ll;         // mega_ll_bytes, zero before the first launch
+  int64_t cap, vocab;
+  int L;
+  float eps;
+};
+int mega_grid();                                   // workgroups per launch; 0 = unsupported device
+bool mega_shape_ok(int hidden, int inter, int hq, int hkv, int head_dim);
+int64_t mega_ll_bytes(int L, int64_t splits, int grid);
+int64_t mega_splits(int64_t cap);
+hipError_t launch_mega_step(const MegaLaunch& m, hipStream_t s);
 int64_t decode_attn_chunk(int64_t cap, int64_t splits);
 void launch_decode_attn(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn, const bf16_t* kn,
                         const bf16_t* cos_t, const bf16_t* sin_t, const int64_t* pos,

@@ -47,6 +47,7 @@ class _Shape:
         self.ids = torch.zeros((B, S), dtype=torch.int64, device=model.device)
         self.ids_host = torch.empty((B, S), dtype=torch.int64, pin_memory=True)
         self.host = torch.empty((max(N, 1), B), dtype=torch.int64, pin_memory=True)
+        self.err_host = torch.zeros((1,), dtype=torch.int32, pin_memory=True)
         self.events = [torch.cuda.Event() for _ in range(max(N, 1))]
         self.graph_ready = False
 
@@ -148,15 +149,28 @@ class Engine:
                 # the step reads tok/pos from the device; capture once per shape
                 sh.decode.capture()
                 sh.graph_ready = True
+        err = sh.decode.err_word
         for t in range(1, N):
             with torch.cuda.stream(self.stream):
                 sh.decode.replay()
                 sh.host[t].copy_(sh.kv.tok, non_blocking=True)
+                if err is not None and t in (1, N - 1):   # the persistent step's error word
+                    sh.err_host.copy_(err, non_blocking=True)
                 sh.events[t].record(self.stream)
             sh.events[t - 1].synchronize()
+            if t - 1 == 1:
+                self._check_step(sh)
             yield sh.host[t - 1].tolist()
         sh.events[N - 1].synchronize()
+        if N > 1:
+            self._check_step(sh)
         yield sh.host[N - 1].tolist()
+
+    @staticmethod
+    def _check_step(sh):
+        if sh.decode.err_word is not None and int(sh.err_host[0]) != 0:
+            raise RuntimeError(f"persistent decode step failed (error word {int(sh.err_host[0])}); "
+                               "QD_MEGA=0 selects the per-launch step")
 
     # -------------------------------------------------------------- tree speculation
     def generate_tree(self, input_ids, max_new_tokens, drafter, T=64):

@@ -73,6 +73,10 @@ SIGNATURES = {
     "qd_fill_bf16": ([p, i64, C.c_uint16, p], i32),
     "qd_decode_workspace_bytes": ([C.POINTER(Weights), i64, i64], i64),
     "qd_decode_step": ([C.POINTER(Weights), C.POINTER(DecodeState), p], i32),
+    "qd_mega_supported": ([C.POINTER(Weights), i64], i32),
+    "qd_mega_workspace_bytes": ([C.POINTER(Weights), i64, i64], i64),
+    "qd_mega_ctl_offset": ([C.POINTER(Weights), i64, i64], i64),
+    "qd_mega_step": ([C.POINTER(Weights), C.POINTER(DecodeState), p], i32),
     "qd_block_workspace_bytes": ([C.POINTER(Weights), i64, i64, i64], i64),
     "qd_block_step": ([C.POINTER(Weights), C.POINTER(BlockState), p], i32),
     "qd_graph_begin": ([p], i32),

@@ -7,12 +7,15 @@ Weights are stacked per kind exactly as the reference packs them (engine/engine.
 The KV cache is [L, B, Hkv, cap, 128] bf16 per K and V (engine.py:178-181).
 
 ``DecodeRunner`` owns the per-step buffers of one batch size and replays the whole decode
-step (qd_decode_step: embed, 36 x 5 launches, LM head + argmax + pos += 1) as one hipGraph;
+step as one hipGraph: at B = 1 on a device that supports it the persistent step (qd_mega_step,
+one launch; ``QD_MEGA=0`` selects the per-launch step), otherwise qd_decode_step (embed,
+36 x 5 launches, LM head + argmax + pos += 1);
 ``BlockRunner`` runs T tokens per sequence through every layer (tree verification, or a causal
 chunk of the prompt).  Every launch goes to the runner's own HIP stream (default priority).
 """
 
 import ctypes as C
+import os
 
 import torch
 
@@ -162,19 +165,39 @@ class KVState:
         self.pos = torch.zeros((1,), dtype=torch.int64, device=dev)
 
 
-class DecodeRunner:
-    """One greedy decode step for all B sequences (qd_decode_step), eager or as a hipGraph."""
+def mega_default(model, batch):
+    """Whether a decode step of `batch` sequences runs as the persistent kernel by default: when
+    the device and shape support it (B = 1), unless QD_MEGA=0 is set."""
+    if os.environ.get("QD_MEGA", "1") == "0":
+        return False
+    return bool(_lib.LIB.qd_mega_supported(C.byref(model.qd), batch))
 
-    def __init__(self, kv, stream):
+
+class DecodeRunner:
+    """One greedy decode step for all B sequences, eager or as a hipGraph: the persistent
+    qd_mega_step (mega=True, B = 1) or qd_decode_step.  mega=None picks mega_default()."""
+
+    def __init__(self, kv, stream, mega=None):
         m = kv.model
         self.kv, self.model, self.stream = kv, m, stream
         B, dev = kv.B, m.device
+        self.mega = mega_default(m, B) if mega is None else bool(mega)
         self.x = torch.empty((B, m.H), dtype=BF16, device=dev)
         self.qkv = torch.empty((B, (m.Hq + 2 * m.Hkv) * 128), dtype=BF16, device=dev)
         self.attn = torch.empty((B, m.Hq * 128), dtype=BF16, device=dev)
         self.act = torch.empty((B, m.I), dtype=BF16, device=dev)
         nbytes = _lib.LIB.qd_decode_workspace_bytes(C.byref(m.qd), B, kv.cap)
+        self.ctl = None
+        if self.mega:
+            nbytes = _lib.LIB.qd_mega_workspace_bytes(C.byref(m.qd), B, kv.cap)
+            if nbytes <= 0:
+                raise _lib.QDError("qd_mega_workspace_bytes", _lib.QD_EARG)
+            self.ctl_off = _lib.LIB.qd_mega_ctl_offset(C.byref(m.qd), B, kv.cap)
+        # zero-filled once: the persistent step's epoch and hand-off words start at 0
         self.ws = torch.zeros((nbytes,), dtype=torch.uint8, device=dev)
+        # device view of the persistent step's error word (None for qd_decode_step)
+        self.err_word = (self.ws[self.ctl_off + 4:self.ctl_off + 8].view(torch.int32)
+                         if self.mega else None)
         self.st = _lib.DecodeState(
             B, kv.cap, kv.k.data_ptr(), kv.v.data_ptr(), kv.cos.data_ptr(), kv.sin.data_ptr(),
             kv.tok.data_ptr(), kv.pos.data_ptr(), self.x.data_ptr(), self.qkv.data_ptr(),
@@ -182,7 +205,22 @@ class DecodeRunner:
         self.graph = None
 
     def enqueue(self):
-        _lib.call("qd_decode_step", C.byref(self.model.qd), C.byref(self.st), self.stream.cuda_stream)
+        fn = "qd_mega_step" if self.mega else "qd_decode_step"
+        _lib.call(fn, C.byref(self.model.qd), C.byref(self.st), self.stream.cuda_stream)
+
+    def mega_status(self):
+        """(epoch, error) words of the persistent step (synchronises the runner's stream)."""
+        if not self.mega:
+            return 0, 0
+        self.stream.synchronize()
+        w = self.ws[self.ctl_off:self.ctl_off + 8].view(torch.int32).cpu().tolist()
+        return w[0], w[1]
+
+    def check(self):
+        """Raise if a persistent step reported an error (expired hand-off wait or bad pos)."""
+        _, err = self.mega_status()
+        if err:
+            raise RuntimeError(f"persistent decode step failed (error word {err})")
 
     def capture(self):
         """Record one step into a hipGraph (the step has no host inputs: tok/pos are on device)."""
