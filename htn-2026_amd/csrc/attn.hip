@@ -38,10 +38,12 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(
   // every prologue load is issued before pos is known: this wave's head row, its norm weights
   // and (ROPE_ROW) the RoPE row; all waves run the same straight-line loads
   auto fetch = [&](HeadVals& hv) -> int64_t {
-    const bf16_t* src = row + attn_head_elem<NW>(wave, kvh, Hq, Hkv);
-    const bf16_t* nw = wave == attn_k_wave<NW>() ? kn : qn;
-    hv.b1 = src[lane]; hv.b2 = src[lane + 64];
-    hv.w1 = bf2f(nw[lane]); hv.w2 = bf2f(nw[lane + 64]);
+    const bf16_t* qsrc = row + attn_q_elem(wave, kvh);
+    const bf16_t* ksrc = row + attn_kv_elem<NW>(wave, kvh, Hq, Hkv);
+    hv.q1 = qsrc[lane]; hv.q2 = qsrc[lane + 64];
+    hv.k1 = ksrc[lane]; hv.k2 = ksrc[lane + 64];
+    hv.qw1 = bf2f(qn[lane]); hv.qw2 = bf2f(qn[lane + 64]);
+    hv.kw1 = bf2f(kn[lane]); hv.kw2 = bf2f(kn[lane + 64]);
     if constexpr (ROPE_ROW) {
       hv.c1 = bf2f(cos_t[lane]); hv.c2 = bf2f(cos_t[lane + 64]);
       hv.s1 = bf2f(sin_t[lane]); hv.s2 = bf2f(sin_t[lane + 64]);
@@ -91,20 +93,17 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict_
   *reinterpret_cast<uint32_t*>(out + r * 128 + lane * 2) = pack2(y.x, y.y);
 }
 
-// Split policy: 16 waves per workgroup take 256 keys per iteration.  One split (no merge launch)
-// while a split has at most ATTN_SPLIT_KEYS keys and the batch alone fills half the CUs;
-// otherwise enough splits of at most ATTN_SPLIT_KEYS keys for ~2 workgroups per CU.
-#ifndef QD_ATTN_NW
-#define QD_ATTN_NW 8
-#endif
-constexpr int ATTN_NW = QD_ATTN_NW;
+// Split policy: ATTN_NW waves per workgroup take ATTN_TILE keys per iteration.  Splits of at
+// most ATTN_SPLIT_KEYS keys; while (batch x KV heads x splits) < 128 workgroups, more splits
+// (whole tiles) up to ~1 workgroup per CU.  Chosen from a sweep on MI355X of {4, 8} waves x
+// splits at B = 1 (cap 768), 4 (cap 8512) and 32 (cap 2176).
 constexpr int64_t ATTN_TILE = ATTN_NW * 16;
-constexpr int64_t ATTN_SPLIT_KEYS = 1024;
+constexpr int64_t ATTN_SPLIT_KEYS = 4096;
 
 int64_t decode_attn_splits(int64_t B, int Hkv, int64_t cap) {
   const int64_t pairs = B * Hkv;
   int64_t sp = (cap + ATTN_SPLIT_KEYS - 1) / ATTN_SPLIT_KEYS;     // bound the keys per split
-  const int64_t fill = (512 + pairs - 1) / pairs;                  // ~2 workgroups per CU
+  const int64_t fill = (256 + pairs - 1) / pairs;                  // ~1 workgroup per CU
   const int64_t max_sp = (cap + ATTN_TILE - 1) / ATTN_TILE;
   if (pairs * sp < 128 && sp < fill) sp = fill < max_sp ? fill : max_sp;
   if (sp < 1) sp = 1;

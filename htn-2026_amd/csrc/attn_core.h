@@ -59,19 +59,19 @@ __device__ __forceinline__ void state_update(SoftmaxState& st, const float (&s)[
   }
 }
 
-// merge the state of lane ^ off into this lane's (all lanes active)
+// merge the state of lane ^ off (off = 16 or 32) into this lane's (all lanes active)
 __device__ __forceinline__ void state_merge_xor(SoftmaxState& st, int off) {
 #pragma unroll
   for (int h = 0; h < GRP; ++h) {
-    const float m2 = __shfl_xor(st.m[h], off, 64);
-    const float l2 = __shfl_xor(st.l[h], off, 64);
+    const float m2 = off == 16 ? lane_xor16(st.m[h]) : lane_xor32(st.m[h]);
+    const float l2 = off == 16 ? lane_xor16(st.l[h]) : lane_xor32(st.l[h]);
     const float mn = fmaxf(st.m[h], m2);
     const float a1 = __expf(st.m[h] - mn);
     const float a2 = __expf(m2 - mn);
     st.l[h] = st.l[h] * a1 + l2 * a2;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float o = __shfl_xor(st.acc[h][e], off, 64);
+      const float o = off == 16 ? lane_xor16(st.acc[h][e]) : lane_xor32(st.acc[h][e]);
       st.acc[h][e] = st.acc[h][e] * a1 + o * a2;
     }
     st.m[h] = mn;
@@ -137,13 +137,13 @@ __device__ __forceinline__ void norm_rope_vals(float x1, float x2, float w1, flo
 }
 
 // One wave's inputs to a decode-attention unit (lane holds dims lane and lane + 64): the raw
-// bf16 values of its head row -- q head `wave` (waves < GRP), the new token's k (wave kw) or v
-// (wave vw) -- the matching norm weights (q_norm, or k_norm for wave kw) and the RoPE values.
-// Every wave loads a full set from valid addresses (a wave with no head reads q head 0 and
-// ignores it): the loads sit in straight-line code with no wave-divergent branch around them.
+// bf16 values of q head kvh * GRP + (wave % GRP) and of the new token's k (v for wave vw), the
+// q_norm / k_norm weights and the RoPE values.  Every wave of a unit loads a full set from valid
+// addresses in straight-line code (no wave-divergent branch around a load) and uses what its
+// role needs.
 struct HeadVals {
-  uint32_t b1 = 0, b2 = 0;          // raw bf16 bits
-  float w1 = 0.f, w2 = 0.f;         // norm weights
+  uint32_t q1 = 0, q2 = 0, k1 = 0, k2 = 0;   // raw bf16 bits (k1/k2 hold v on wave vw)
+  float qw1 = 0.f, qw2 = 0.f, kw1 = 0.f, kw2 = 0.f;
   float c1 = 0.f, c2 = 0.f, s1 = 0.f, s2 = 0.f;
 };
 
@@ -161,15 +161,14 @@ __device__ __forceinline__ constexpr int attn_k_wave() { return NW > GRP ? GRP :
 template <int NW>
 __device__ __forceinline__ constexpr int attn_v_wave() { return NW > GRP + 1 ? GRP + 1 : 1; }
 
-// Element offset, within a packed qkv row ([Hq | Hkv | Hkv] heads of 128), of the head row that
-// `wave` reads for KV head kvh (waves with no head read q head kvh * GRP), and whether it uses
-// k_norm.  Pure selects: no branch.
+// Element offsets, within a packed qkv row ([Hq | Hkv | Hkv] heads of 128), of the q head and
+// of the k (or, for wave vw, v) head that `wave` reads for KV head kvh.  Pure arithmetic.
+__device__ __forceinline__ int64_t attn_q_elem(int wave, int kvh) {
+  return (int64_t)(kvh * GRP + (wave & (GRP - 1))) * 128;
+}
 template <int NW>
-__device__ __forceinline__ int64_t attn_head_elem(int wave, int kvh, int Hq, int Hkv) {
-  const int hq = kvh * GRP + (wave < GRP ? wave : 0);
-  const int head = wave == attn_k_wave<NW>() ? Hq + kvh
-                   : wave == attn_v_wave<NW>() ? Hq + Hkv + kvh : hq;
-  return (int64_t)head * 128;
+__device__ __forceinline__ int64_t attn_kv_elem(int wave, int kvh, int Hq, int Hkv) {
+  return (int64_t)(Hq + (wave == attn_v_wave<NW>() ? Hkv : 0) + kvh) * 128;
 }
 
 // One (sequence, KV head, key split) unit over keys [start, start + chunk) of one layer's cache
@@ -180,6 +179,8 @@ __device__ __forceinline__ int64_t attn_head_elem(int wave, int kvh, int Hq, int
 // final(h, d, y0, y1) with the normalised output dims d, d+1 of head h when `whole` (the unit
 // covers every key), else partial(h, d, A0, A1, M, L) with the unnormalised accumulators and
 // the (max, sum) pair.  The last step runs on waves 0..3 only (threads 0..255, one head each).
+// In a workgroup of more than NW waves, the waves past NW do no work but run the unit's
+// barriers (fetch must return pos for them too).
 template <int NW, class Fetch, class Final, class Partial>
 __device__ __forceinline__ void decode_attn_unit(DecodeAttnLds<NW>& sm, const Fetch& fetch,
                                                  const Final& final_out,
@@ -189,21 +190,24 @@ __device__ __forceinline__ void decode_attn_unit(DecodeAttnLds<NW>& sm, const Fe
                                                  float eps, float scale) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, i = lane & 15;
+  const bool act = wave < NW;             // waves past NW only take part in the barriers
   const uint4* kb = reinterpret_cast<const uint4*>(k_cache + head_off);
   const uint4* vb = reinterpret_cast<const uint4*>(v_cache + head_off);
   constexpr int TILE = NW * GRP * KPG;    // keys per workgroup iteration
   constexpr int kw = attn_k_wave<NW>(), vw = attn_v_wave<NW>();
   uint4 kx[KPG], vx[KPG];
   int64_t j0 = start + (int64_t)wave * GRP * KPG;
+  if (act) {
 #pragma unroll
-  for (int kk = 0; kk < KPG; ++kk) {
-    const int64_t j = j0 + g * KPG + kk;
-    const int64_t jj = j < cap ? j : cap - 1;
-    kx[kk] = kb[jj * 16 + i];
-    vx[kk] = vb[jj * 16 + i];
+    for (int kk = 0; kk < KPG; ++kk) {
+      const int64_t j = j0 + g * KPG + kk;
+      const int64_t jj = j < cap ? j : cap - 1;
+      kx[kk] = kb[jj * 16 + i];
+      vx[kk] = vb[jj * 16 + i];
+    }
   }
   HeadVals hv;
-  const int64_t pos = fetch(hv);
+  const int64_t pos = fetch(hv);          // every wave: fetch loads nothing for waves past NW
   if (pos < 0 || pos >= cap) return;  // uniform over the unit: no slot to write
   const int64_t kend = min(start + chunk, pos);  // cached keys only; `pos` is the new token
   bool ok[KPG];
@@ -211,7 +215,7 @@ __device__ __forceinline__ void decode_attn_unit(DecodeAttnLds<NW>& sm, const Fe
   for (int kk = 0; kk < KPG; ++kk) ok[kk] = j0 + g * KPG + kk < kend;
   if (wave < GRP) {
     float o1, o2;
-    norm_rope_vals(bf2f(hv.b1), bf2f(hv.b2), hv.w1, hv.w2, hv.c1, hv.c2, hv.s1, hv.s2, eps, o1,
+    norm_rope_vals(bf2f(hv.q1), bf2f(hv.q2), hv.qw1, hv.qw2, hv.c1, hv.c2, hv.s1, hv.s2, eps, o1,
                    o2);
     // lane l holds dims l and l + 64; repack as bf16 pairs through LDS
     reinterpret_cast<bf16_t*>(sm.qs[wave])[lane] = (bf16_t)f2bf(o1);
@@ -220,7 +224,7 @@ __device__ __forceinline__ void decode_attn_unit(DecodeAttnLds<NW>& sm, const Fe
   const bool owns = pos >= start && pos < start + chunk;
   if (owns && wave == kw) {
     float o1, o2;
-    norm_rope_vals(bf2f(hv.b1), bf2f(hv.b2), hv.w1, hv.w2, hv.c1, hv.c2, hv.s1, hv.s2, eps, o1,
+    norm_rope_vals(bf2f(hv.k1), bf2f(hv.k2), hv.kw1, hv.kw2, hv.c1, hv.c2, hv.s1, hv.s2, eps, o1,
                    o2);
     const bf16_t k1 = (bf16_t)f2bf(o1), k2 = (bf16_t)f2bf(o2);
     k_cache[head_off + pos * 128 + lane] = k1;
@@ -229,12 +233,13 @@ __device__ __forceinline__ void decode_attn_unit(DecodeAttnLds<NW>& sm, const Fe
     reinterpret_cast<bf16_t*>(sm.kns)[lane + 64] = k2;
   }
   if (owns && wave == vw) {
-    v_cache[head_off + pos * 128 + lane] = (bf16_t)hv.b1;
-    v_cache[head_off + pos * 128 + lane + 64] = (bf16_t)hv.b2;
-    sm.vnew[lane] = bf2f(hv.b1);
-    sm.vnew[lane + 64] = bf2f(hv.b2);
+    v_cache[head_off + pos * 128 + lane] = (bf16_t)hv.k1;
+    v_cache[head_off + pos * 128 + lane + 64] = (bf16_t)hv.k2;
+    sm.vnew[lane] = bf2f(hv.k1);
+    sm.vnew[lane + 64] = bf2f(hv.k2);
   }
   lds_barrier();
+  if (act) {
   uint4 qp[GRP];
 #pragma unroll
   for (int h = 0; h < GRP; ++h) qp[h] = reinterpret_cast<const uint4*>(sm.qs[h])[i];
@@ -293,6 +298,7 @@ __device__ __forceinline__ void decode_attn_unit(DecodeAttnLds<NW>& sm, const Fe
 #pragma unroll
     for (int h = 0; h < GRP; ++h) { sm.wm[wave][h] = st.m[h]; sm.wl[wave][h] = st.l[h]; }
   }
+  }  // act
   lds_barrier();
   if (tid >= 256) return;                 // 4 waves combine: one per head, 2 dims per lane
   const int h = tid >> 6, d = (tid & 63) * 2;

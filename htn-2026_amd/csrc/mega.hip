@@ -183,7 +183,7 @@ struct Smem {
   float rown[16];                  // residual values of the workgroup's o / down rows
   float best_v[MG_NW];
   int32_t best_i[MG_NW];
-  DecodeAttnLds<MG_NW> attn;
+  DecodeAttnLds<ATTN_NW> attn;
 };
 
 // the workgroup's outputs obuf[0, nrows) -> LL words [w0, w0 + nrows / 2) of dst
@@ -250,19 +250,27 @@ __device__ void phase_attn_unit(const MegaParams& p, Smem& sm, int l, int unit, 
   uint32_t* err = p.ctl + 1;
   const uint64_t* qkv = LL + ly.qkv;
   auto fetch = [&](HeadVals& hv) -> int64_t {
-    // element e of the packed qkv row lives in word e / 2, half e & 1; every wave reads a head
-    // row (straight-line code, no wave-divergent branch around a load or wait)
-    const int64_t e = attn_head_elem<MG_NW>(wave, kvh, HQ, HKV);
-    const uint64_t* w1 = qkv + ((e + lane) >> 1);
-    const uint64_t* w2 = qkv + ((e + lane + 64) >> 1);
-    const uint64_t r1 = ll_raw(w1), r2 = ll_raw(w2);
-    const bf16_t* nw = (wave == attn_k_wave<MG_NW>() ? p.k_norm : p.q_norm) + (int64_t)l * HD;
-    hv.w1 = bf2f(nw[lane]); hv.w2 = bf2f(nw[lane + 64]);
-    hv.c1 = bf2f(p.cos[pos * HD + lane]); hv.c2 = bf2f(p.cos[pos * HD + lane + 64]);
-    hv.s1 = bf2f(p.sin[pos * HD + lane]); hv.s2 = bf2f(p.sin[pos * HD + lane + 64]);
-    const uint32_t u1 = ll_wait(r1, w1, tag, err), u2 = ll_wait(r2, w2, tag, err);
-    hv.b1 = (lane & 1) ? u1 >> 16 : u1 & 0xFFFF;
-    hv.b2 = (lane & 1) ? u2 >> 16 : u2 & 0xFFFF;
+    // element e of the packed qkv row lives in word e / 2, half e & 1; the unit's waves read
+    // their q and k (v) rows in straight-line code, the other waves nothing
+    if (wave < ATTN_NW) {
+      const int64_t eq = attn_q_elem(wave, kvh), ek = attn_kv_elem<ATTN_NW>(wave, kvh, HQ, HKV);
+      const uint64_t* wq1 = qkv + ((eq + lane) >> 1);
+      const uint64_t* wq2 = qkv + ((eq + lane + 64) >> 1);
+      const uint64_t* wk1 = qkv + ((ek + lane) >> 1);
+      const uint64_t* wk2 = qkv + ((ek + lane + 64) >> 1);
+      const uint64_t rq1 = ll_raw(wq1), rq2 = ll_raw(wq2), rk1 = ll_raw(wk1), rk2 = ll_raw(wk2);
+      const bf16_t* qn = p.q_norm + (int64_t)l * HD;
+      const bf16_t* kn = p.k_norm + (int64_t)l * HD;
+      hv.qw1 = bf2f(qn[lane]); hv.qw2 = bf2f(qn[lane + 64]);
+      hv.kw1 = bf2f(kn[lane]); hv.kw2 = bf2f(kn[lane + 64]);
+      hv.c1 = bf2f(p.cos[pos * HD + lane]); hv.c2 = bf2f(p.cos[pos * HD + lane + 64]);
+      hv.s1 = bf2f(p.sin[pos * HD + lane]); hv.s2 = bf2f(p.sin[pos * HD + lane + 64]);
+      const uint32_t sh = (lane & 1) * 16;
+      hv.q1 = (ll_wait(rq1, wq1, tag, err) >> sh) & 0xFFFF;
+      hv.q2 = (ll_wait(rq2, wq2, tag, err) >> sh) & 0xFFFF;
+      hv.k1 = (ll_wait(rk1, wk1, tag, err) >> sh) & 0xFFFF;
+      hv.k2 = (ll_wait(rk2, wk2, tag, err) >> sh) & 0xFFFF;
+    }
     return pos;
   };
   auto final_out = [&](int h, int d, float y0, float y1) {
@@ -277,7 +285,7 @@ __device__ void phase_attn_unit(const MegaParams& p, Smem& sm, int l, int unit, 
       ll_put(LL + ly.ml + idx * 2 + 1, __float_as_uint(Lsum), tag);
     }
   };
-  decode_attn_unit<MG_NW>(sm.attn, fetch, final_out, partial_out,
+  decode_attn_unit<ATTN_NW>(sm.attn, fetch, final_out, partial_out,
                           p.k_cache + (int64_t)l * layer_kv, p.v_cache + (int64_t)l * layer_kv,
                           (int64_t)kvh * p.cap * HD, p.cap, (int64_t)split * p.chunk, p.chunk,
                           p.splits == 1, p.eps, 1.0f / sqrtf((float)HD));
@@ -321,8 +329,12 @@ __device__ void phase_merge(const MegaParams& p, int l, int hq, uint32_t tag) {
   ll_put(LL + ly.att + (int64_t)hq * (HD / 2) + lane, pack2(y.x, y.y), tag);
 }
 
-// mid = x + bf16(attn . Wo^T)   (10 rows: waves 0..7, waves 0, 1 take a second row)
-__device__ void phase_o(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t tag) {
+// mid = x + bf16(attn . Wo^T)   (10 rows: waves 0..7, waves 0, 1 take a second row), then
+// act = bf16(silu(bf16(g))) * bf16(u), g / u = RMSNorm(mid; ln2) . Wgate / Wup^T (act rows
+// wave + 8 rr of the workgroup's 38).  The first two act rows' gate/up weights are loaded
+// together with the o rows, before the attention output is awaited, so they stream during the
+// attention hand-offs; later act rows are double-buffered.
+__device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t tag) {
   const int wave = threadIdx.x >> 6;
   const Layout ly = ll_layout(p.L, p.splits);
   uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
@@ -330,11 +342,24 @@ __device__ void phase_o(const MegaParams& p, Smem& sm, int l, int wg, int P, uin
   part_range(H / 2, wg, P, a, b);
   const int64_t r0 = 2 * a;
   const int nr = (int)(2 * (b - a));
+  int64_t ga, gb;
+  part_range(INTER / 2, wg, P, ga, gb);
+  const int64_t g0 = 2 * ga;
+  const int ng = (int)(2 * (gb - ga));
   const bf16_t* W = p.w_o + (int64_t)l * H * (HQ * HD);
-  uint4 w[2][8];
+  const bf16_t* WG = p.w_gu + (int64_t)l * 2 * INTER * H;
+  constexpr int RW = 5;            // act rows per wave (<= 38 per workgroup)
+  uint4 w[2][8], g[2][5], u[2][5];
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr)
     if (wave + rr * MG_NW < nr) mg_load_row<8>(W, r0 + wave + rr * MG_NW, w[rr]);
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    if (wave + rr * MG_NW < ng) {
+      mg_load_row<5>(WG, g0 + wave + rr * MG_NW, g[rr]);
+      mg_load_row<5>(WG, g0 + wave + rr * MG_NW + INTER, u[rr]);
+    }
+  }
   ll_fetch_lds<4>(LL + ly.att, HQ * HD / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
   lds_barrier();
 #pragma unroll
@@ -347,54 +372,30 @@ __device__ void phase_o(const MegaParams& p, Smem& sm, int l, int wg, int P, uin
   }
   lds_barrier();
   put_pairs(sm, LL + ly.mid, a, nr, tag);
-}
-
-// act = bf16(silu(bf16(g))) * bf16(u), g / u = RMSNorm(mid; ln2) . Wgate / Wup^T
-// (act rows wave + 8 rr of the workgroup's 38; two rows' weights in flight per wave)
-__device__ void phase_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t tag) {
-  const int wave = threadIdx.x >> 6;
-  const Layout ly = ll_layout(p.L, p.splits);
-  uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
-  int64_t a, b;
-  part_range(INTER / 2, wg, P, a, b);
-  const int64_t r0 = 2 * a;
-  const int nr = (int)(2 * (b - a));
-  const bf16_t* W = p.w_gu + (int64_t)l * 2 * INTER * H;
-  constexpr int RW = 5;            // act rows per wave (<= 38 per workgroup)
-  uint4 g[2][5], u[2][5];
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int k = wave + rr * MG_NW;
-    if (k < nr) {
-      mg_load_row<5>(W, r0 + k, g[rr]);
-      mg_load_row<5>(W, r0 + k + INTER, u[rr]);
-    }
-  }
+  // ---- gate/up + SwiGLU
   ll_fetch_lds<3>(LL + ly.mid, H / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
   lds_barrier();
   {                                // residual values of this workgroup's down rows
-    int64_t da, db;
-    part_range(H / 2, wg, P, da, db);
     const int t = threadIdx.x;
-    if (t < 2 * (db - da)) sm.rown[t] = bf2f(reinterpret_cast<const bf16_t*>(sm.xs)[2 * da + t]);
+    if (t < nr) sm.rown[t] = bf2f(reinterpret_cast<const bf16_t*>(sm.xs)[r0 + t]);
   }
   mg_norm<5, 512>(sm.xs, p.ln2 + (int64_t)l * H, p.eps, sm.red);
 #pragma unroll
   for (int rr = 0; rr < RW; ++rr) {
     const int k = wave + rr * MG_NW;
-    if (k < nr) {
+    if (k < ng) {
       const float ag = mg_dot<5>(g[rr & 1], sm.xs);
       const float au = mg_dot<5>(u[rr & 1], sm.xs);
       const int kn = k + 2 * MG_NW;
-      if (rr + 2 < RW && kn < nr) {
-        mg_load_row<5>(W, r0 + kn, g[rr & 1]);
-        mg_load_row<5>(W, r0 + kn + INTER, u[rr & 1]);
+      if (rr + 2 < RW && kn < ng) {
+        mg_load_row<5>(WG, g0 + kn, g[rr & 1]);
+        mg_load_row<5>(WG, g0 + kn + INTER, u[rr & 1]);
       }
       if ((threadIdx.x & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(rbf(silu_f(rbf(ag))) * rbf(au));
     }
   }
   lds_barrier();
-  put_pairs(sm, LL + ly.act, a, nr, tag);
+  put_pairs(sm, LL + ly.act, ga, ng, tag);
 }
 
 // out = mid + bf16(act . Wdown^T)   (10 rows as phase_o)
@@ -528,8 +529,7 @@ __global__ __launch_bounds__(MG_NT) void mega_step_kernel(MegaParams p) {
     phase_qkv(p, sm, l, wg, P, tag, tok);
     for (int u = wg; u < units; u += P) phase_attn_unit(p, sm, l, u, tag, pos);
     if (p.splits > 1 && wg >= merge0 && wave == 0) phase_merge(p, l, wg - merge0, tag);
-    phase_o(p, sm, l, wg, P, tag);
-    phase_gu(p, sm, l, wg, P, tag);
+    phase_o_gu(p, sm, l, wg, P, tag);
     phase_down(p, sm, l, wg, P, tag);
   }
   phase_lm(p, sm, wg, P, tag);

@@ -39,15 +39,34 @@ __device__ __forceinline__ float row16_sum_dpp(float v) {
   v += QD_DPP(v, 0x140);
   return v;
 }
+// v of lane ^ 16 / lane ^ 32 with gfx950's v_permlane16_swap / v_permlane32_swap (one VALU op
+// each instead of an LDS-crossbar ds_bpermute).  With both operands = v, permlane16_swap
+// returns (v with its odd rows replaced by the even rows, v with its even rows replaced by the
+// odd rows); permlane32_swap does the same for the two 32-lane halves.  Every lane must be
+// active.
+__device__ __forceinline__ float lane_xor16(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
 __device__ __forceinline__ float wave_sum(float v) {
   v = row16_sum_dpp(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
+  v += lane_xor16(v);
+  v += lane_xor32(v);
   return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  v = fmaxf(v, lane_xor32(v));
+  v = fmaxf(v, lane_xor16(v));
+  v = fmaxf(v, QD_DPP(v, 0xB1));
+  v = fmaxf(v, QD_DPP(v, 0x4E));
+  v = fmaxf(v, QD_DPP(v, 0x141));
+  v = fmaxf(v, QD_DPP(v, 0x140));
   return v;
 }
 // sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15)

@@ -54,6 +54,11 @@ void launch_gemm(const bf16_t* x, int64_t x_stride, int64_t M, const bf16_t* w, 
                  int epi, float* pval, int32_t* pidx, float* logits, hipStream_t s);
 
 // attn.hip
+// waves per decode-attention unit (4 query heads x 16 keys per wave per iteration)
+#ifndef QD_ATTN_NW
+#define QD_ATTN_NW 4
+#endif
+constexpr int ATTN_NW = QD_ATTN_NW;
 int64_t decode_attn_splits(int64_t B, int Hkv, int64_t cap);
 
 // persistent B = 1 decode step (mega.hip)
