@@ -9,12 +9,16 @@ Workloads:
   b32    config 4 -- 36 layers, B=32, prompts of 2048, up to 128 new tokens (same method).
 Weights are seeded random-init N(0, 0.02) generated on the device; prompt ids uniform.
 
-Roofline: the dominant kernel (gate/up GEMV + SwiGLU) is timed live with HIP events on the
-engine's stream, as a hipGraph of its 36 per-layer launches (each on its own layer's weights,
-so nothing is cache resident) replayed R times; achieved = algorithmic bytes per launch / mean
-launch time.  ``step_roofline`` does the same for the whole step: weights + KV read per step /
-step time.  cpu_baseline times the CPU oracle (oracle/qwen3_ref.py, same architecture and
-generator) on this host's cores on a bounded sample.
+Roofline: at B=1 the step is ONE kernel (mega_step_kernel, the persistent decode step), so
+the dominant kernel is the step itself: achieved = algorithmic bytes per step (weights + the
+KV read, averaged over the timed steps) / mean launch duration, timed live with HIP events on
+the engine's stream around the K graph replays (one kernel node each).  With QD_MEGA=0 (the
+per-launch step) the dominant kernel is the gate/up GEMV + SwiGLU, timed as a hipGraph of its 36
+per-layer launches (each on its own layer's weights, so nothing is cache resident) replayed R
+times; that figure is always reported as ``gemv_gate_up``.  ``traffic`` is HBM bytes per launch
+from rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by a 512 MiB copy (profiles/).  cpu_baseline
+times the CPU oracle (oracle/qwen3_ref.py, same architecture and generator) on this host's
+cores on a bounded sample.
 """
 
 import argparse
@@ -32,6 +36,10 @@ PEAK_HBM_GBS = 8000.0
 # factors being what the same counters read for a 512 MiB device copy.  Summary and commands:
 # profiles/gemv_gate_up_b1_traffic.md.
 GU_TRAFFIC_B1 = 99_771_853
+# HBM bytes per persistent-step launch at B=1 (config 3), same method (FETCH_SIZE x 1.99986 +
+# WRITE_SIZE), mean over the profiled steps at positions 512..520; summary and commands:
+# profiles/mega_step_b1_traffic.md.
+MEGA_TRAFFIC_B1 = 8_272_170_585
 METRIC = "decode tok/s (Qwen3-4B bf16, B=1 & B=32) + achieved HBM GB/s vs peak"
 
 
@@ -80,6 +88,7 @@ def decode_run(eng, B, S, N, warmup, steps, seed):
     step_bytes = eng.model.weight_bytes + kv_bytes
     return sh, {"B": B, "S": S, "K": K, "ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / K,
                 "step": "qd_mega_step (persistent)" if sh.decode.mega else "qd_decode_step",
+                "mega": sh.decode.mega,
                 "tok_s": B * 1e3 / ms, "prefill_s": prefill_s, "bytes_per_step": step_bytes,
                 "achieved_gbs": step_bytes / (ms * 1e-3) / 1e9}
 
@@ -229,6 +238,18 @@ def main():
         log(f"cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} threads")
 
     gu_gbs = gu_bytes / (us * 1e-6) / 1e9
+    gemv = {"bound": "hbm", "kernel": "gemv_kernel gate/up + SwiGLU (B=1, per-launch step)",
+            "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": GU_TRAFFIC_B1,
+            "bytes_per_launch": gu_bytes, "us_per_launch": round(us, 3)}
+    if r1["mega"]:
+        roofline = {"bound": "hbm", "kernel": "mega_step_kernel (whole B=1 decode step)",
+                    "achieved": round(r1["achieved_gbs"], 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(r1["achieved_gbs"] / PEAK_HBM_GBS, 4),
+                    "traffic": MEGA_TRAFFIC_B1, "bytes_per_launch": int(r1["bytes_per_step"]),
+                    "us_per_launch": round(r1["ms_per_step"] * 1e3, 2)}
+    else:
+        roofline = gemv
     line = {
         "metric": METRIC, "value": round(r1["tok_s"], 2), "unit": "tok/s", "n_gpus": 1,
         "steps": r1["K"], "warmup": a.warmup, "ms_per_step": round(r1["ms_per_step"], 5),
@@ -239,10 +260,8 @@ def main():
                                "N=256 greedy decode (steps timed after prefill)",
                    "batch": 1, "prompt_len": 512, "new_tokens": 256, "layers": 36,
                    "decode_step": r1["step"]},
-        "roofline": {"bound": "hbm", "kernel": "gemv gate/up + SwiGLU (B=1)",
-                     "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": GU_TRAFFIC_B1,
-                     "bytes_per_launch": gu_bytes, "us_per_launch": round(us, 3)},
+        "roofline": roofline,
+        "gemv_gate_up": gemv,
         "step_roofline": {"bound": "hbm", "achieved": round(r1["achieved_gbs"], 1),
                           "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(r1["achieved_gbs"] / PEAK_HBM_GBS, 4),
