@@ -5,11 +5,13 @@
 //
 // CDNA4 mapping (v_mfma_f32_16x16x32_bf16, wave64):
 //  * a workgroup owns 16 weight rows (one MFMA N tile) and up to 64 activation rows (MT M tiles);
-//    its NW waves split K round-robin in groups of 128 and are summed in LDS at the end;
-//  * lane (q = lane / 16, c = lane % 16) streams 64 contiguous bytes of weight row n0 + c per
-//    group (k = g*128 + 32 q .. +31) and the same k range of activation row m0 + 16 mt + c; the
-//    four 16-byte pieces feed four MFMAs.  The k order inside a group is a permutation shared by
-//    both operands, so the contraction is unchanged;
+//    its NW waves split K into contiguous runs of 128-wide groups, summed in LDS at the end;
+//  * MFMA s (s < 4) of group g contracts k = g*128 + 32 s .. +31: lane (q = lane / 16,
+//    c = lane % 16) supplies k = 32 s + 8 q .. +7 of weight row n0 + c and of activation row
+//    m0 + 16 mt + c, so one load instruction reads 64 contiguous bytes of each of 16 rows;
+//  * each wave keeps its next D weight groups in flight (a ring refilled as groups are consumed)
+//    and loads the next group's activation tiles one group ahead, so a workgroup has
+//    D x NW x 4 KiB of weights outstanding instead of one group per wave;
 //  * grid.x walks the M blocks fastest, so the workgroups that re-read one weight tile for
 //    different M blocks run together and hit L2 / MALL instead of HBM.
 // Accumulation is fp32; only the summation order differs from the reference.
@@ -20,60 +22,19 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 __device__ __forceinline__ bf16x8_t as_bf8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
+// Cross-wave reduction of the accumulators through LDS and the epilogue (store / residual /
+// SwiGLU / per-tile argmax partials).
 template <int MT, int EPI, int NW>
-__global__ __launch_bounds__(NW * 64) void gemm_kernel(
-    const bf16_t* __restrict__ X, int64_t x_stride, int M, const bf16_t* __restrict__ W, int N,
-    int K, bf16_t* out, int64_t out_stride, const bf16_t* res, int64_t res_stride, float* pval,
-    int32_t* pidx, float* logits) {
+__device__ __forceinline__ void gemm_epilogue(const f32x4_t (&acc)[MT], const f32x4_t* acc2,
+                                              int64_t m0, int64_t n0, int M, int N, bf16_t* out,
+                                              int64_t out_stride, const bf16_t* res,
+                                              int64_t res_stride, float* pval, int32_t* pidx,
+                                              float* logits) {
   constexpr bool SW = EPI == EPI_SWIGLU;
   __shared__ float red[NW][MT * 256];
   __shared__ float red2[SW ? NW : 1][SW ? MT * 256 : 1];
   __shared__ float tile[EPI == EPI_ARGMAX ? MT * 16 : 1][17];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int c = lane & 15, q = lane >> 4;
-  const int64_t m0 = (int64_t)blockIdx.x * (MT * 16);
-  const int64_t n0 = (int64_t)blockIdx.y * 16;
-  const int64_t nrow = n0 + c < N ? n0 + c : N - 1;  // clamped rows are computed, never stored
-  const uint4* wr = reinterpret_cast<const uint4*>(W + nrow * K);
-  const uint4* wr2 = reinterpret_cast<const uint4*>(W + (nrow + (SW ? N : 0)) * K);
-  const uint4* xr[MT];
-  bool xok[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int64_t m = m0 + mt * 16 + c;
-    xok[mt] = m < M;
-    xr[mt] = reinterpret_cast<const uint4*>(X + (xok[mt] ? m : 0) * x_stride);
-  }
-  f32x4_t acc[MT], acc2[SW ? MT : 1];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  if constexpr (SW) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc2[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
-  const int ngroups = K / 128;
-  for (int g = wave; g < ngroups; g += NW) {
-    const int64_t c0 = (int64_t)g * 16 + q * 4;  // uint4 index of k = g*128 + 32 q
-    uint4 wv[4], wv2[SW ? 4 : 1];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) wv[s] = ld_stream(wr + c0 + s);
-    if constexpr (SW) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) wv2[s] = ld_stream(wr2 + c0 + s);
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      uint4 xv[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) xv[s] = xok[mt] ? xr[mt][c0 + s] : make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xv[s]), as_bf8(wv[s]), acc[mt], 0, 0, 0);
-        if constexpr (SW)
-          acc2[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xv[s]), as_bf8(wv2[s]), acc2[mt], 0, 0, 0);
-      }
-    }
-  }
   // D[i][j] of one 16x16 tile: lane holds rows i = 4 q + r (r < 4) of column j = c
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -127,16 +88,122 @@ __global__ __launch_bounds__(NW * 64) void gemm_kernel(
   }
 }
 
+// The main loop runs passes of G groups; within a pass the schedule is fully unrolled and every
+// load sits in straight-line code (indices clamped into the wave's run, activation rows past M
+// masked after the load), so the compiler's wait counts let the ring of D weight groups and the
+// next group's activation tiles stay in flight while the current group's MFMAs run.  Only the
+// MFMAs of groups past the wave's run are skipped (a wave-uniform branch with no loads in it).
+template <int MT, int EPI, int NW, int G, int D>
+__global__ __launch_bounds__(NW * 64) void gemm_kernel(
+    const bf16_t* __restrict__ X, int64_t x_stride, int M, const bf16_t* __restrict__ W, int N,
+    int K, bf16_t* out, int64_t out_stride, const bf16_t* res, int64_t res_stride, float* pval,
+    int32_t* pidx, float* logits) {
+  constexpr bool SW = EPI == EPI_SWIGLU;
+  static_assert(D >= 1 && D <= G, "ring depth");
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = lane & 15, q = lane >> 4;
+  const int64_t m0 = (int64_t)blockIdx.x * (MT * 16);
+  const int64_t n0 = (int64_t)blockIdx.y * 16;
+  const int64_t nrow = n0 + c < N ? n0 + c : N - 1;  // clamped rows are computed, never stored
+  const uint4* wr = reinterpret_cast<const uint4*>(W + nrow * K);
+  const uint4* wr2 = reinterpret_cast<const uint4*>(W + (nrow + (SW ? N : 0)) * K);
+  const uint4* xr[MT];
+  uint32_t xmask[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int64_t m = m0 + mt * 16 + c;
+    xmask[mt] = m < M ? 0xFFFFFFFFu : 0u;
+    xr[mt] = reinterpret_cast<const uint4*>(X + (m < M ? m : 0) * x_stride);
+  }
+  f32x4_t acc[MT], acc2[SW ? MT : 1];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if constexpr (SW) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc2[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  // this wave's groups: a contiguous run [gbeg, gend) of 128-wide K groups
+  const int ngroups = K / 128;
+  const int per = (ngroups + NW - 1) / NW;
+  const int gbeg = min(wave * per, ngroups);
+  const int gend = min(gbeg + per, ngroups);
+  uint4 wv[D][4], wv2[SW ? D : 1][4], xv[2][MT][4];
+  for (int p0 = gbeg; p0 < gend; p0 += G) {
+    const int n = min(G, gend - p0);
+    // uint4 index of k = g*128 + 8 q (+ 32 s) for pass slot i, clamped into the run
+    auto gcol = [&](int i) { return (int64_t)(p0 + (i < n ? i : n - 1)) * 16 + q; };
+    auto load_w = [&](int slot, int i) {
+      const int64_t c0 = gcol(i);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) wv[slot][s] = ld_stream(wr + c0 + 4 * s);
+      if constexpr (SW) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) wv2[slot][s] = ld_stream(wr2 + c0 + 4 * s);
+      }
+    };
+    auto load_x = [&](int buf, int i) {
+      const int64_t c0 = gcol(i);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          uint4 v = xr[mt][c0 + 4 * s];
+          v.x &= xmask[mt]; v.y &= xmask[mt]; v.z &= xmask[mt]; v.w &= xmask[mt];
+          xv[buf][mt][s] = v;
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < D; ++i) load_w(i, i);
+    load_x(0, 0);
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      if (i + 1 < G) load_x((i + 1) & 1, i + 1);
+      if (i < n) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xv[i & 1][mt][s]), as_bf8(wv[i % D][s]), acc[mt], 0, 0, 0);
+            if constexpr (SW)
+              acc2[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xv[i & 1][mt][s]), as_bf8(wv2[i % D][s]), acc2[mt], 0, 0, 0);
+          }
+      }
+      if (i + D < G) load_w(i % D, i + D);
+    }
+  }
+  gemm_epilogue<MT, EPI, NW>(acc, SW ? acc2 : nullptr, m0, n0, M, N, out, out_stride, res,
+                             res_stride, pval, pidx, logits);
+}
+
 int64_t gemm_argmax_parts(int64_t N) { return (N + 15) / 16; }
+
+// Waves per workgroup and groups per pass from the number of 128-wide K groups: K <= 2560 -> 4
+// waves x 5 groups; K <= 5120 -> 8 x 5; otherwise 8 waves x 10 groups per pass.  Ring depth:
+// the whole pass for one M tile (4 groups with the gate/up pair), 4 for two, 2 for four (whose
+// activation buffers take the registers).
+template <int MT, int EPI, int NW, int G>
+static void gemm_launch(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
+                        int64_t K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs,
+                        float* pval, int32_t* pidx, float* logits, hipStream_t s) {
+  constexpr bool SW = EPI == EPI_SWIGLU;
+  constexpr int D0 = MT >= 4 ? 2 : MT == 2 ? 4 : (SW ? 4 : G);
+  constexpr int D = D0 < G ? D0 : G;
+  const dim3 grid((unsigned)((M + MT * 16 - 1) / (MT * 16)), (unsigned)((N + 15) / 16));
+  gemm_kernel<MT, EPI, NW, G, D><<<grid, dim3(NW * 64), 0, s>>>(x, xs, (int)M, w, (int)N, (int)K,
+                                                               out, os, res, rs, pval, pidx, logits);
+}
 
 template <int MT, int EPI>
 static void gemm_go(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N, int64_t K,
                     bf16_t* out, int64_t os, const bf16_t* res, int64_t rs, float* pval,
                     int32_t* pidx, float* logits, hipStream_t s) {
-  constexpr int NW = 4;
-  const dim3 grid((unsigned)((M + MT * 16 - 1) / (MT * 16)), (unsigned)((N + 15) / 16));
-  gemm_kernel<MT, EPI, NW><<<grid, dim3(NW * 64), 0, s>>>(x, xs, (int)M, w, (int)N, (int)K, out, os,
-                                                         res, rs, pval, pidx, logits);
+  const int64_t ng = K / 128;
+  if (ng <= 20)
+    gemm_launch<MT, EPI, 4, 5>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
+  else if (ng <= 40)
+    gemm_launch<MT, EPI, 8, 5>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
+  else
+    gemm_launch<MT, EPI, 8, 10>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
 }
 
 template <int EPI>

@@ -4,7 +4,9 @@ transformers run (tests/golden/config1.json) and the CPU oracle.
 Token rule (north star): ids identical at every step where the reference top-2 margin exceeds
 1e-2.  The reference logits for a step are taken teacher-forced on the engine's own prefix
 (the judge's replay, QWEN_ENGINE_CONTRACT.md:105-123), so a legitimate near-tie flip is judged
-on what was actually generated."""
+on what was actually generated.  Against the stored golden run, whose margins are bf16 logit
+differences, a margin of at most one bf16 ulp of the top logit counts as a tie (it bounds the
+fp32 margin by nothing: any summation order may flip it)."""
 
 import hashlib
 import json
@@ -14,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import GOLDEN, ORACLE_TIE, ensure_oracle_built, margin_rule
+from helpers import GOLDEN, ORACLE_TIE, bf16_ulp, ensure_oracle_built, margin_rule
 from oracle import qwen3_ref as R
 from oracle import synth
 
@@ -59,13 +61,20 @@ def test_config1_greedy(eng4, ref4):
     assert len(steps) == 32 and all(len(s) == 1 for s in steps)
     toks = np.array(steps).T                                     # [B, N]
     gold = np.array(CFG1["tokens"])
-    first_tie = next((i for i, m in enumerate(CFG1["margins"]) if m <= 1e-2), 32)
+    # The golden margins are differences of bf16 logits.  At |logit| ~ 4 the bf16 spacing is
+    # 0.03125, above the rule's 1e-2, and a one-ulp bf16 gap can come from an fp32 gap of any
+    # size down to ~1e-6 -- so a margin of at most one ulp of the top logit is a rounding tie
+    # that any fp32 summation order may flip.  Wider margins must match.
+    def tied(i):
+        top = torch.tensor(CFG1["top_values"][i][0], dtype=torch.float32)
+        return CFG1["margins"][i] <= max(1e-2, float(bf16_ulp(top)))
+    first_tie = next((i for i in range(32) if tied(i)), 32)
     assert np.array_equal(toks[0, :first_tie], gold[0, :first_tie]), (toks, gold)
     # the north-star rule against transformers itself: the prefix is identical to the golden
     # run up to the first divergence, so the golden margins apply there verbatim
     div = next((i for i in range(32) if toks[0, i] != gold[0, i]), 32)
     if div < 32:
-        assert CFG1["margins"][div] <= 1e-2, f"diverged at step {div}, golden margin {CFG1['margins'][div]}"
+        assert tied(div), f"diverged at step {div}, golden margin {CFG1['margins'][div]}"
     tl = ref4.teacher_logits(np.array(prompt), toks)
     bad = margin_rule(toks, tl, margin=ORACLE_TIE)
     worst = float((tl.float().max(-1).values - tl.float().gather(-1, torch.as_tensor(toks)[..., None])[..., 0]).max())
@@ -132,10 +141,13 @@ def test_tree_verification_is_exact(eng2, ref2):
 
     def drafter(seq, T):
         t = tr.branching_tree(seq[-1], T, (4, 4, 2, 2), lambda n: rng.integers(0, 151936, size=n))
-        b = next(i for i in range(2) if cont[i][:len(seq)] == list(seq))
-        truth = cont[b][len(seq):len(seq) + 4]
+        b = next(i for i in range(2) if cont[i][:48] == list(seq[:48]))   # the row, by its prompt
+        # the plain run's continuation while the tree run still follows it (a near-tie flip
+        # between the two kernels' summation orders ends that; random drafts from then on)
+        truth = cont[b][len(seq):len(seq) + 4] if cont[b][:len(seq)] == list(seq) else []
         t2 = tr.Tree(seq[-1])
-        t2.add_path(truth, T)
+        if truth:
+            t2.add_path(truth, T)
         for i in range(1, len(t.tokens)):
             if len(t2.tokens) >= T:
                 break
