@@ -25,15 +25,22 @@ __device__ __forceinline__ bf16x8_t as_bf8(uint4 v) { return __builtin_bit_cast(
 // Cross-wave reduction of the accumulators through LDS and the epilogue (store / residual /
 // SwiGLU / per-tile argmax partials).
 template <int MT, int EPI, int NW>
-__device__ __forceinline__ void gemm_epilogue(const f32x4_t (&acc)[MT], const f32x4_t* acc2,
-                                              int64_t m0, int64_t n0, int M, int N, bf16_t* out,
-                                              int64_t out_stride, const bf16_t* res,
-                                              int64_t res_stride, float* pval, int32_t* pidx,
-                                              float* logits) {
+struct EpiLds {
+  float red[NW][MT * 256];
+  float red2[EPI == EPI_SWIGLU ? NW : 1][EPI == EPI_SWIGLU ? MT * 256 : 1];
+  float tile[EPI == EPI_ARGMAX ? MT * 16 : 1][17];
+};
+
+template <int MT, int EPI, int NW>
+__device__ __forceinline__ void gemm_epilogue(EpiLds<MT, EPI, NW>& sm, const f32x4_t (&acc)[MT],
+                                              const f32x4_t* acc2, int64_t m0, int64_t n0, int M,
+                                              int N, bf16_t* out, int64_t out_stride,
+                                              const bf16_t* res, int64_t res_stride, float* pval,
+                                              int32_t* pidx, float* logits) {
   constexpr bool SW = EPI == EPI_SWIGLU;
-  __shared__ float red[NW][MT * 256];
-  __shared__ float red2[SW ? NW : 1][SW ? MT * 256 : 1];
-  __shared__ float tile[EPI == EPI_ARGMAX ? MT * 16 : 1][17];
+  auto& red = sm.red;
+  auto& red2 = sm.red2;
+  auto& tile = sm.tile;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // D[i][j] of one 16x16 tile: lane holds rows i = 4 q + r (r < 4) of column j = c
 #pragma unroll
@@ -171,8 +178,112 @@ __global__ __launch_bounds__(NW * 64) void gemm_kernel(
       if (i + D < G) load_w(i % D, i + D);
     }
   }
-  gemm_epilogue<MT, EPI, NW>(acc, SW ? acc2 : nullptr, m0, n0, M, N, out, out_stride, res,
+  __shared__ EpiLds<MT, EPI, NW> esm;
+  gemm_epilogue<MT, EPI, NW>(esm, acc, SW ? acc2 : nullptr, m0, n0, M, N, out, out_stride, res,
                              res_stride, pval, pidx, logits);
+}
+
+// ------------------------------------------------------------------ LDS-staged kernel (M <= 64)
+// One 16-row weight tile (gate and up tiles for SwiGLU) x one block of MT*16 activation rows per
+// workgroup of 8 waves, K in 512-wide chunks (K % 512 == 0).  Each chunk of every staged row
+// (weight rows, then activation rows) is one 1 KiB-contiguous load instruction -- lane i loads
+// 16-byte unit i -- written to LDS at unit i ^ (row & 15), so the MFMA fragment reads (16 rows x
+// one 64-byte k slice) hit 16 distinct bank groups.  Wave w contracts k slices 2w and 2w + 1 of
+// each chunk,
+// and the waves' accumulators are summed in LDS at the end (gemm_epilogue).  NB chunks are in
+// flight in registers (a ring refilled as each chunk is staged).  Weights stream from
+// HBM in 1 KiB pieces and each activation row is read once per workgroup.
+template <int MT, int EPI, int NB>
+__global__ __launch_bounds__(512) void gemm_lds_kernel(
+    const bf16_t* __restrict__ X, int64_t x_stride, int M, const bf16_t* __restrict__ W, int N,
+    int K, bf16_t* out, int64_t out_stride, const bf16_t* res, int64_t res_stride, float* pval,
+    int32_t* pidx, float* logits) {
+  constexpr bool SW = EPI == EPI_SWIGLU;
+  constexpr int NWV = 8;
+  constexpr int WR = SW ? 32 : 16;               // staged weight rows
+  constexpr int XR = MT * 16;                    // staged activation rows
+  constexpr int R = WR + XR;
+  static_assert(R % NWV == 0, "rows per wave");
+  constexpr int LPW = R / NWV;                   // row-chunk loads per wave per chunk
+  __shared__ uint4 stage[R * 64];                // R rows x 64 units of 16 B (512 k)
+  __shared__ EpiLds<MT, EPI, NWV> esm;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = lane & 15, q = lane >> 4;
+  const int64_t m0 = (int64_t)blockIdx.x * XR;
+  const int64_t n0 = (int64_t)blockIdx.y * 16;
+  // source row of each of this wave's staged rows rr = wave + 8 j (clamped rows load valid data
+  // whose results are never stored)
+  const uint4* src[LPW];
+  bool wrow[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) {
+    const int rr = wave + NWV * j;
+    if (rr < WR) {
+      const int64_t nr = n0 + (rr & 15) < N ? n0 + (rr & 15) : N - 1;
+      src[j] = reinterpret_cast<const uint4*>(W + (nr + (rr >= 16 ? N : 0)) * (int64_t)K);
+      wrow[j] = true;
+    } else {
+      const int64_t mr = m0 + (rr - WR) < M ? m0 + (rr - WR) : M - 1;
+      src[j] = reinterpret_cast<const uint4*>(X + mr * x_stride);
+      wrow[j] = false;
+    }
+  }
+  const int nchunks = K / 512;
+  uint4 buf[NB][LPW];
+  auto load = [&](int b, int kc) {
+#pragma unroll
+    for (int j = 0; j < LPW; ++j)
+      buf[b][j] = wrow[j] ? ld_stream(src[j] + (int64_t)kc * 64 + lane) : src[j][(int64_t)kc * 64 + lane];
+  };
+  auto store = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int rr = wave + NWV * j;
+      stage[rr * 64 + (lane ^ (rr & 15))] = buf[b][j];
+    }
+  };
+  f32x4_t acc[MT], acc2[SW ? MT : 1];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if constexpr (SW) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc2[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  auto compute = [&]() {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int u = (4 * (2 * wave + t) + q) ^ c;  // unit of k slice 2w + t, quarter q, row c
+      const uint4 wf = stage[c * 64 + u];
+      uint4 uf;
+      if constexpr (SW) uf = stage[(16 + c) * 64 + u];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint4 xf = stage[(WR + 16 * mt + c) * 64 + u];
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xf), as_bf8(wf), acc[mt], 0, 0, 0);
+        if constexpr (SW)
+          acc2[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xf), as_bf8(uf), acc2[mt], 0, 0, 0);
+      }
+    }
+  };
+  // chunk k is staged from buf[k % NB]; chunk k + NB is then loaded into the same registers
+  // (prefetches past the end re-load the last chunk: every load stays unconditional)
+#pragma unroll
+  for (int b = 0; b < NB; ++b) load(b, min(b, nchunks - 1));
+  for (int kc = 0; kc < nchunks; kc += NB) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int k = kc + b;
+      if (k < nchunks) {
+        lds_barrier();                           // the previous chunk's fragments are read
+        store(b);
+        load(b, min(k + NB, nchunks - 1));
+        lds_barrier();                           // this chunk is staged
+        compute();
+      }
+    }
+  }
+  gemm_epilogue<MT, EPI, NWV>(esm, acc, SW ? acc2 : nullptr, m0, n0, M, N, out, out_stride, res,
+                              res_stride, pval, pidx, logits);
 }
 
 int64_t gemm_argmax_parts(int64_t N) { return (N + 15) / 16; }
@@ -206,10 +317,27 @@ static void gemm_go(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int
     gemm_launch<MT, EPI, 8, 10>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
 }
 
+#ifndef QD_GEMM_NB
+#define QD_GEMM_NB 2
+#endif
+template <int MT, int EPI, int NB = QD_GEMM_NB>
+static void gemm_lds_go(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
+                        int64_t K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs,
+                        float* pval, int32_t* pidx, float* logits, hipStream_t s) {
+  const dim3 grid((unsigned)((M + MT * 16 - 1) / (MT * 16)), (unsigned)((N + 15) / 16));
+  gemm_lds_kernel<MT, EPI, NB><<<grid, dim3(512), 0, s>>>(x, xs, (int)M, w, (int)N, (int)K, out,
+                                                          os, res, rs, pval, pidx, logits);
+}
+
 template <int EPI>
 static void gemm_mt(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N, int64_t K,
                     bf16_t* out, int64_t os, const bf16_t* res, int64_t rs, float* pval,
                     int32_t* pidx, float* logits, hipStream_t s) {
+  if (M <= 64 && K % 512 == 0) {
+    if (M <= 16) gemm_lds_go<1, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
+    else gemm_lds_go<2, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
+    return;
+  }
   if (M <= 16) gemm_go<1, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
   else if (M <= 32) gemm_go<2, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
   else gemm_go<4, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
