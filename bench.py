@@ -1,12 +1,15 @@
 """Decode benchmark on one MI355X: Qwen3-4B-shaped bf16 greedy decode through the HIP engine.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-b32] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-b32] [--no-tree] [--no-cpu]
 
 Workloads:
   value  config 3 -- 36 layers, B=1, prompt 512, up to 256 new tokens: decode tok/s over K timed
          steps (one step = one hipGraph replay of the whole decode step: embed, 36 layers,
          LM head + argmax), after W warm-up steps; inputs resident in HBM.
   b32    config 4 -- 36 layers, B=32, prompts of 2048, up to 128 new tokens (same method).
+  tree   config 5 -- tree verification, B=4, context 8192, 64-node random trees: the verify
+         forward timed with HIP events (bytes/s and MFMA TFLOP/s), plus an end-to-end
+         generate_tree (tokens per pass, wall-clock tok/s).
 Weights are seeded random-init N(0, 0.02) generated on the device; prompt ids uniform.
 
 Roofline: at B=1 the step is ONE kernel (mega_step_kernel, the persistent decode step), so
@@ -93,6 +96,77 @@ def decode_run(eng, B, S, N, warmup, steps, seed):
                 "achieved_gbs": step_bytes / (ms * 1e-3) / 1e9}
 
 
+def tree_run(eng, B=4, S=8192, T=64, K=20, warmup=3, N_e2e=64, seed=5):
+    """Config 5: tree verification.  Prefill B prompts of S tokens, draft one random T-node tree
+    per sequence (qdecode.tree.random_tree_drafter, branching 4-4-2-2), then time K replays of
+    the verify forward (qd_block_step over B*T rows: every weight once + every row's K/V) with
+    HIP events on the engine's stream.  Then an end-to-end generate_tree of N_e2e tokens (wall
+    clock, drafting / accept walk / per-pass sync included) for tokens per pass."""
+    import numpy as np
+    import torch
+    from qdecode import tree as tr
+    rng = np.random.default_rng(seed)
+    ids = torch.as_tensor(rng.integers(0, eng.model.V, size=(B, S)), dtype=torch.int64)
+    eng.tree_T = T
+    try:
+        eng.shape = None
+        sh = eng._state(B, S, N_e2e)
+    finally:
+        eng.tree_T = 0
+    st = eng.stream
+    t0 = time.perf_counter()
+    with torch.cuda.stream(st):
+        sh.ids.copy_(ids)
+        sh.run_prefill()
+    st.synchronize()
+    prefill_s = time.perf_counter() - t0
+    first = sh.kv.tok.cpu().tolist()
+    drafter = tr.random_tree_drafter(seed)
+    trees = [drafter(list(map(int, ids[b])) + [first[b]], T) for b in range(B)]
+    run = sh.tree
+    with torch.cuda.stream(st):
+        run.tokens.copy_(torch.tensor([t.tokens for t in trees], dtype=torch.int64))
+        run.depth.copy_(torch.tensor([t.depth for t in trees], dtype=torch.int64))
+        run.anc.copy_(torch.tensor([t.anc_i64() for t in trees], dtype=torch.int64))
+        run.base.fill_(S)
+        for _ in range(warmup):
+            run.enqueue(T)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(st):
+        e0.record(st)
+        for _ in range(K):
+            run.enqueue(T)
+        e1.record(st)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / K
+    m = eng.model
+    ctx = S + T
+    kv_bytes = B * S * m.kv_bytes_per_token
+    nbytes = m.weight_bytes + kv_bytes
+    dense = 36 * (6144 * 2560 + 2560 * 4096 + 19456 * 2560 + 2560 * 9728) + m.V * m.H
+    gemm_flop = 2.0 * B * T * dense
+    attn_flop = 4.0 * B * T * 32 * 128 * ctx * m.L
+    # end to end (same shape, host loop included)
+    prompt = ids.tolist()
+    w0 = time.perf_counter()
+    out = list(eng.generate_tree(prompt, N_e2e, tr.random_tree_drafter(seed + 1), T=T))
+    wall = time.perf_counter() - w0
+    stats = eng.tree_stats
+    acc = stats["accepted"]
+    return {"workload": f"config 5: tree verification, B={B}, context {S}, {T}-node random "
+                        f"4-4-2-2 trees", "verify_ms": round(ms, 4), "verify_steps": K,
+            "bytes_per_verify": int(nbytes), "achieved_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "gemm_tflop_per_verify": round(gemm_flop / 1e12, 3),
+            "attn_tflop_per_verify": round(attn_flop / 1e12, 3),
+            "achieved_tflops": round((gemm_flop + attn_flop) / (ms * 1e-3) / 1e12, 1),
+            "mfma_frac": round((gemm_flop + attn_flop) / (ms * 1e-3) / 2.5e15, 4),
+            "prefill_s": round(prefill_s, 3),
+            "e2e": {"new_tokens": N_e2e, "passes": stats["passes"],
+                    "tokens_per_pass": round(sum(acc) / max(len(acc), 1), 3),
+                    "wall_s": round(wall, 3), "tok_s": round(B * len(out) / wall, 1)}}
+
+
 def time_gu_kernel(eng, sh, reps=20):
     """Mean duration of the gate/up GEMV + SwiGLU launch (B rows) over all layers' weights."""
     import ctypes as C
@@ -175,6 +249,7 @@ def main():
     ap.add_argument("--b32-steps", type=int, default=100)
     ap.add_argument("--no-b32", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-tree", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB: the reference "
@@ -230,6 +305,17 @@ def main():
         del sh32
         torch.cuda.empty_cache()
 
+    tree = None
+    if not a.no_tree:
+        eng.shape = None
+        torch.cuda.empty_cache()
+        tree = tree_run(eng)
+        log(f"tree verify (B=4, ctx 8192, T=64): {tree['verify_ms']:.3f} ms, "
+            f"{tree['achieved_gbs']:.0f} GB/s, {tree['achieved_tflops']:.1f} TFLOP/s; "
+            f"e2e {tree['e2e']['tok_s']} tok/s, prefill {tree['prefill_s']:.2f}s")
+        eng.shape = None
+        torch.cuda.empty_cache()
+
     cpu = None
     if not a.no_cpu:
         eng = None
@@ -269,6 +355,7 @@ def main():
         "wall_ms_per_step": round(r1["wall_ms_per_step"], 5),
         "prefill_s": round(r1["prefill_s"], 3),
         "b32": b32,
+        "tree": tree,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -198,6 +198,181 @@ __global__ __launch_bounds__(256) void block_attn_kernel(
   }
 }
 
+// MFMA version (v_mfma_f32_16x16x32_bf16).  Workgroup = (key split of BLOCK_CHUNK keys, KV
+// head, block of BA_TQ query tokens of one sequence); wave w handles query head kvh*4 + w for the
+// block's tokens (two 16-row tiles).  Keys go in tiles of 32:
+//  * S' = K . Q^T: A = K tile rows (LDS, 16-byte units XOR-swizzled by key), B = the lane's query
+//    row (registers); lane (c, q) ends up holding the scores of its query row c against keys
+//    4q..4q+3 and 16+4q..16+4q+3 of the tile;
+//  * online softmax per query row in fp32 (the row max / sum across the four q lanes through
+//    permlane swaps), P rounded to bf16;
+//  * O^T += V^T . P^T: A = V^T rows (LDS, stored transposed with a padded stride), B = the lane's
+//    8 probabilities, taken in that same key order (a permutation of the contraction index shared
+//    by both operands), so O^T's lane (c, q) holds dims 16 dt + 4q..+3 of row c and the per-row
+//    rescale needs no cross-lane traffic;
+//  * the next key tile is loaded into registers while the current one is consumed.
+// Writes (m, l, acc) partials per (row, split) like block_attn_kernel; attn_merge_kernel merges.
+constexpr int BA_TQ = 32;
+constexpr int BA_VT = 36;  // V^T row stride (bf16): 72 bytes, 16 rows hit 32 distinct banks
+
+__global__ __launch_bounds__(256) void block_attn_mfma_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
+    const bf16_t* __restrict__ v_cache, const int64_t* __restrict__ base_ptr,
+    const uint64_t* __restrict__ anc, int64_t T, int Hq, int Hkv, int64_t cap, float scale,
+    float* ws_acc, float* ws_ml) {
+  typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+  typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+  __shared__ uint4 ks[32 * 16];
+  __shared__ bf16_t vt[128 * BA_VT];
+  const int split = blockIdx.x, kvh = blockIdx.y;
+  const int splits = gridDim.x;
+  const int64_t QB = (T + BA_TQ - 1) / BA_TQ;
+  const int64_t b = blockIdx.z / QB;
+  const int64_t t0 = (blockIdx.z % QB) * BA_TQ;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = lane & 15, q4 = lane >> 4;
+  const int64_t base = base_ptr[b];
+  // query rows of this lane: token t0 + 16 rt + c, head kvh * 4 + wave
+  uint4 qf[2][4];
+  uint64_t mask[2];
+  int64_t tok[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    tok[rt] = t0 + 16 * rt + c;
+    const int64_t tt = tok[rt] < T ? tok[rt] : T - 1;
+    const uint4* qr = reinterpret_cast<const uint4*>(q + ((b * T + tt) * Hq + kvh * GRP + wave) * 128);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) qf[rt][kk] = qr[4 * kk + q4];
+    mask[rt] = anc ? anc[b * T + tt] : 0;
+  }
+  const int64_t start = (int64_t)split * BLOCK_CHUNK;
+  int64_t kend = start + BLOCK_CHUNK;
+  if (kend > base + T) kend = base + T;
+  if (!anc && kend > base + t0 + BA_TQ) kend = base + t0 + BA_TQ;   // causal: later keys unseen
+  if (kend > cap) kend = cap;
+  const int64_t head_off = ((b * Hkv + kvh) * cap) * 128;
+  const uint4* kb = reinterpret_cast<const uint4*>(k_cache + head_off);
+  const uint4* vb = reinterpret_cast<const uint4*>(v_cache + head_off);
+  float m[2] = {M_FLOOR, M_FLOOR}, lsum[2] = {0.f, 0.f};
+  f32x4_t o[2][8];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[rt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // staging: thread tid moves units 2 tid, 2 tid + 1 of the 32 x 16-unit K and V tiles (key
+  // tid / 8, units 2 (tid % 8) and 2 (tid % 8) + 1)
+  const int skey = tid >> 3, su = 2 * (tid & 7);
+  uint4 kx0, kx1, vx0, vx1;
+  {
+    const int64_t j = start + skey < cap ? start + skey : cap - 1;
+    kx0 = kb[j * 16 + su]; kx1 = kb[j * 16 + su + 1];
+    vx0 = vb[j * 16 + su]; vx1 = vb[j * 16 + su + 1];
+  }
+  for (int64_t j0 = start; j0 < kend; j0 += 32) {
+    lds_barrier();                                     // the previous tile is consumed
+    ks[skey * 16 + (su ^ (skey & 15))] = kx0;
+    ks[skey * 16 + ((su + 1) ^ (skey & 15))] = kx1;
+    {
+      bf16_t* col = vt + 8 * su * BA_VT + skey;
+      col[0 * BA_VT] = (bf16_t)(vx0.x & 0xFFFF); col[1 * BA_VT] = (bf16_t)(vx0.x >> 16);
+      col[2 * BA_VT] = (bf16_t)(vx0.y & 0xFFFF); col[3 * BA_VT] = (bf16_t)(vx0.y >> 16);
+      col[4 * BA_VT] = (bf16_t)(vx0.z & 0xFFFF); col[5 * BA_VT] = (bf16_t)(vx0.z >> 16);
+      col[6 * BA_VT] = (bf16_t)(vx0.w & 0xFFFF); col[7 * BA_VT] = (bf16_t)(vx0.w >> 16);
+      col += 8 * BA_VT;
+      col[0 * BA_VT] = (bf16_t)(vx1.x & 0xFFFF); col[1 * BA_VT] = (bf16_t)(vx1.x >> 16);
+      col[2 * BA_VT] = (bf16_t)(vx1.y & 0xFFFF); col[3 * BA_VT] = (bf16_t)(vx1.y >> 16);
+      col[4 * BA_VT] = (bf16_t)(vx1.z & 0xFFFF); col[5 * BA_VT] = (bf16_t)(vx1.z >> 16);
+      col[6 * BA_VT] = (bf16_t)(vx1.w & 0xFFFF); col[7 * BA_VT] = (bf16_t)(vx1.w >> 16);
+    }
+    lds_barrier();                                     // the tile is staged
+    {                                                  // next tile (clamped: always a load)
+      const int64_t jn = j0 + 32 + skey;
+      const int64_t j = jn < cap ? jn : cap - 1;
+      kx0 = kb[j * 16 + su]; kx1 = kb[j * 16 + su + 1];
+      vx0 = vb[j * 16 + su]; vx1 = vb[j * 16 + su + 1];
+    }
+    // S' = K . Q^T for both key halves and both row tiles
+    f32x4_t sc[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) sc[rt][h2] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int key = 16 * h2 + c;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const uint4 kf = ks[key * 16 + ((4 * kk + q4) ^ c)];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+          sc[rt][h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, kf), __builtin_bit_cast(bf16x8_t, qf[rt][kk]),
+              sc[rt][h2], 0, 0, 0);
+      }
+    }
+    // online softmax of both row tiles; P packed in the key order {4q4..+3, 16+4q4..+3}
+    uint4 pf[2];
+    float alpha[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float sv[8];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t j = j0 + 16 * h2 + 4 * q4 + r;
+          bool vis = j < kend;
+          if (j >= base) {
+            const int64_t jb = j - base;
+            vis = vis && (anc ? jb < 64 && ((mask[rt] >> (jb & 63)) & 1ull) != 0 : jb <= tok[rt]);
+          }
+          sv[4 * h2 + r] = vis ? sc[rt][h2][r] * scale : NEG_INF;
+        }
+      float mx = sv[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
+      mx = fmaxf(mx, lane_xor16(mx));
+      mx = fmaxf(mx, lane_xor32(mx));
+      const float mn = fmaxf(m[rt], mx);
+      alpha[rt] = __expf(m[rt] - mn);
+      m[rt] = mn;
+      float p[8], ps = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { p[e] = __expf(sv[e] - mn); ps += p[e]; }
+      lsum[rt] = lsum[rt] * alpha[rt] + ps;
+      pf[rt] = make_uint4(pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7]));
+    }
+    // O^T += V^T . P^T: V^T fragment of dims 16 dt + c, keys 4q4..+3 and 16+4q4..+3
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const bf16_t* row = vt + (16 * dt + c) * BA_VT;
+      const uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * q4);
+      const uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * q4);
+      const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        o[rt][dt] *= alpha[rt];
+        o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8_t, vf), __builtin_bit_cast(bf16x8_t, pf[rt]), o[rt][dt], 0,
+            0, 0);
+      }
+    }
+  }
+  // per-row totals: the four q lanes of a row hold disjoint key subsets of l
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    float l = lsum[rt];
+    l += lane_xor16(l);
+    l += lane_xor32(l);
+    if (tok[rt] >= T) continue;
+    const int64_t idx = ((b * T + tok[rt]) * Hq + kvh * GRP + wave) * splits + split;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      *reinterpret_cast<f32x4_t*>(ws_acc + idx * 128 + 16 * dt + 4 * q4) = o[rt][dt];
+    if (q4 == 0) { ws_ml[idx * 2] = m[rt]; ws_ml[idx * 2 + 1] = l; }
+  }
+}
+
 int64_t block_attn_splits(int64_t cap) { return (cap + BLOCK_CHUNK - 1) / BLOCK_CHUNK; }
 
 void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
@@ -205,9 +380,10 @@ void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_c
                        int Hkv, int64_t cap, int64_t splits, float* ws_acc, float* ws_ml,
                        bf16_t* out, hipStream_t s) {
   if (B * T <= 0) return;
-  const int64_t TQ = (T + 3) / 4;
-  block_attn_kernel<<<dim3((unsigned)splits, (unsigned)Hkv, (unsigned)(B * TQ)), dim3(256), 0, s>>>(
-      q, k_cache, v_cache, base, anc, T, Hq, Hkv, cap, 1.0f / sqrtf(128.0f), ws_acc, ws_ml);
+  const int64_t QB = (T + BA_TQ - 1) / BA_TQ;
+  block_attn_mfma_kernel<<<dim3((unsigned)splits, (unsigned)Hkv, (unsigned)(B * QB)), dim3(256), 0,
+                           s>>>(q, k_cache, v_cache, base, anc, T, Hq, Hkv, cap,
+                                1.0f / sqrtf(128.0f), ws_acc, ws_ml);
   attn_merge_kernel<<<dim3((unsigned)(B * T * Hq)), dim3(64), 0, s>>>(ws_acc, ws_ml, (int)splits,
                                                                       out);
 }
