@@ -330,27 +330,39 @@ static void gemm_lds_go(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w,
 }
 
 template <int EPI>
-static void gemm_mt(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N, int64_t K,
-                    bf16_t* out, int64_t os, const bf16_t* res, int64_t rs, float* pval,
-                    int32_t* pidx, float* logits, hipStream_t s) {
+static int64_t gemm_mt(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
+                       int64_t K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs,
+                       float* pval, int32_t* pidx, float* logits, float* part, int64_t part_floats,
+                       hipStream_t s) {
+  if (M >= GEMM_TILE_MIN_M && gemm_tile_ok(M, N, K, EPI, x, xs, w, out, os, res, rs))
+    return launch_gemm_tile(x, xs, M, w, N, K, out, os, res, rs, EPI, pval, pidx, logits, part,
+                            part_floats, s);
   if (M <= 64 && K % 512 == 0) {
     if (M <= 16) gemm_lds_go<1, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
     else gemm_lds_go<2, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
-    return;
+  } else if (M <= 16) {
+    gemm_go<1, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
+  } else if (M <= 32) {
+    gemm_go<2, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
+  } else {
+    gemm_go<4, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
   }
-  if (M <= 16) gemm_go<1, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
-  else if (M <= 32) gemm_go<2, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
-  else gemm_go<4, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
+  return EPI == EPI_ARGMAX ? gemm_argmax_parts(N) : 0;
 }
 
-void launch_gemm(const bf16_t* x, int64_t x_stride, int64_t M, const bf16_t* w, int64_t N,
-                 int64_t K, bf16_t* out, int64_t out_stride, const bf16_t* res, int64_t res_stride,
-                 int epi, float* pval, int32_t* pidx, float* logits, hipStream_t s) {
-  if (M <= 0) return;
+int64_t launch_gemm(const bf16_t* x, int64_t x_stride, int64_t M, const bf16_t* w, int64_t N,
+                    int64_t K, bf16_t* out, int64_t out_stride, const bf16_t* res,
+                    int64_t res_stride, int epi, float* pval, int32_t* pidx, float* logits,
+                    hipStream_t s, float* part, int64_t part_floats) {
+  if (M <= 0) return 0;
+#define QD_MT(E) \
+  gemm_mt<E>(x, x_stride, M, w, N, K, out, out_stride, res, res_stride, pval, pidx, logits, part, \
+             part_floats, s)
   switch (epi) {
-    case EPI_RES: gemm_mt<EPI_RES>(x, x_stride, M, w, N, K, out, out_stride, res, res_stride, pval, pidx, logits, s); break;
-    case EPI_SWIGLU: gemm_mt<EPI_SWIGLU>(x, x_stride, M, w, N, K, out, out_stride, res, res_stride, pval, pidx, logits, s); break;
-    case EPI_ARGMAX: gemm_mt<EPI_ARGMAX>(x, x_stride, M, w, N, K, out, out_stride, res, res_stride, pval, pidx, logits, s); break;
-    default: gemm_mt<EPI_NONE>(x, x_stride, M, w, N, K, out, out_stride, res, res_stride, pval, pidx, logits, s); break;
+    case EPI_RES: return QD_MT(EPI_RES);
+    case EPI_SWIGLU: return QD_MT(EPI_SWIGLU);
+    case EPI_ARGMAX: return QD_MT(EPI_ARGMAX);
+    default: return QD_MT(EPI_NONE);
   }
+#undef QD_MT
 }

@@ -1,0 +1,364 @@
+// LDS-tiled MFMA GEMM for many activation rows (tree verification B*T rows, prefill chunks):
+//   out[m, n] = epi( sum_k X[m, k] * W[n, k] )
+// with the epilogues of the decode GEMM (store / residual / SwiGLU / per-tile argmax for the LM
+// head) -- the large-M counterpart of the reference's tensor-core GEMMs (gemv.py:61-116 with
+// BLOCK_M >= 16, fast.py:161-213) and of its cuBLAS prefill (engine.py:550-592).
+//
+// CDNA4 mapping (v_mfma_f32_16x16x32_bf16, wave64, 160 KiB LDS per CU):
+//  * a workgroup of 4 waves owns a 128 (weight rows) x 128 (activation rows) output tile; wave
+//    (wn, wm) owns the 64 x 64 quarter (4 x 4 MFMA tiles, 64 fp32 accumulators per lane);
+//  * K advances in stages of 64: both 128-row x 128-byte tiles are staged in LDS, each row as 8
+//    16-byte units stored at unit ^ (row & 7), so the fragment reads (16 rows x one 16-byte unit)
+//    and the staging writes (8 rows x 8 units per 8 lanes) hit distinct banks;
+//  * two LDS buffers (64 KiB, two workgroups per CU) and a two-deep register ring: the global
+//    loads of stage s + 2 are issued before stage s is contracted, stage s + 1 is written to the
+//    other buffer after it, so one barrier per stage and two stages of loads in flight;
+//  * A = weight rows, B = activation rows: the accumulator lane (c, q) holds output columns
+//    n..n+3 (4 q + r) of row m (c), so every epilogue store is one 8-byte write;
+//  * workgroup ids are remapped so the tiles that one XCD runs are consecutive in (M block
+//    fastest, then N block): the M blocks that share a weight tile run on one XCD and meet in its
+//    L2 instead of each XCD fetching the tile from HBM;
+//  * when the tile grid is too small to fill the chip (few rows, narrow N), K is split over
+//    workgroups; the fp32 partial tiles go to a caller-provided workspace and a second kernel
+//    sums them in split order and applies the epilogue (deterministic).
+// Requirements (checked by gemm_tile_ok): K % 64 == 0, N % 128 == 0 (SwiGLU: N % 64 == 0),
+// 16-byte aligned X / W rows, 8-byte aligned output / residual rows.
+#include "qd_launch.h"
+
+namespace {
+
+constexpr int TM = 128, TN = 128, TK = 64;
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+__device__ __forceinline__ bf16x8_t as_bf8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+struct TileLds {
+  uint4 w[2][TN * 8];
+  uint4 x[2][TM * 8];
+};
+
+// one stage of one thread's staging units: 4 weight and 4 activation 16-byte units (named
+// registers: arrays here end up in scratch or LDS)
+struct Stage {
+  uint4 w0, w1, w2, w3, x0, x1, x2, x3;
+};
+struct Src {
+  const uint4 *W, *X;
+  int64_t w0, w1, w2, w3, x0, x1, x2, x3;   // uint4 offsets of the thread's 4 + 4 rows
+};
+__device__ __forceinline__ void load_stage(Stage& st, const Src& s, int64_t kk) {
+  st.w0 = ld_stream(s.W + s.w0 + kk);
+  st.w1 = ld_stream(s.W + s.w1 + kk);
+  st.w2 = ld_stream(s.W + s.w2 + kk);
+  st.w3 = ld_stream(s.W + s.w3 + kk);
+  st.x0 = s.X[s.x0 + kk];
+  st.x1 = s.X[s.x1 + kk];
+  st.x2 = s.X[s.x2 + kk];
+  st.x3 = s.X[s.x3 + kk];
+}
+__device__ __forceinline__ void store_stage(const Stage& st, uint4* lw, uint4* lx) {
+  lw[0] = st.w0;
+  lw[256] = st.w1;
+  lw[512] = st.w2;
+  lw[768] = st.w3;
+  lx[0] = st.x0;
+  lx[256] = st.x1;
+  lx[512] = st.x2;
+  lx[768] = st.x3;
+}
+
+template <int EPI, bool SPLIT>
+__global__ __launch_bounds__(256, 2) void gemm_tile_kernel(
+    const bf16_t* __restrict__ X, int64_t x_stride, int M, const bf16_t* __restrict__ W, int N,
+    int K, int mblocks, int nblocks, int ks_per, bf16_t* out, int64_t out_stride, const bf16_t* res,
+    int64_t res_stride, float* pval, int32_t* pidx, float* logits, float* part) {
+  __shared__ TileLds sm;
+  __shared__ float amax_v[2][2][64];
+  __shared__ int32_t amax_i[2][2][64];
+  // XCD-aware remap: hardware workgroup h runs on XCD h % 8; give each XCD a contiguous run of
+  // logical tiles
+  const int total = gridDim.x, h = blockIdx.x;
+  const int xq = total >> 3, xr = total & 7, xcd = h & 7, slot = h >> 3;
+  const int L = xcd < xr ? xcd * (xq + 1) + slot : xr * (xq + 1) + (xcd - xr) * xq + slot;
+  const int mb = L % mblocks;
+  const int nb = (L / mblocks) % nblocks;
+  const int split = L / (mblocks * nblocks);
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = lane & 15, q = lane >> 4;
+  const int wn = wave & 1, wm = wave >> 1;
+  const int64_t m0 = (int64_t)mb * TM;
+  const int ksteps = K / TK;
+  const int kbeg = split * ks_per;
+  const int kend = min(ksteps, kbeg + ks_per);
+
+  // staging: thread tid moves units u = tid + 256 i (i < 4) of both tiles: row r0 + 32 i
+  // (r0 = tid / 8), unit tid % 8.  Weight row of LDS row r0 + 32 i: nb*128 + r0 + 32 i, or for
+  // SwiGLU (gate | up halves of W, 64 output columns per block) nb*64 + r0 + 32 (i / 2) plus N
+  // for odd i (the up rows).
+  const int r0 = tid >> 3, unit0 = tid & 7;
+  const int Nrows = EPI == EPI_SWIGLU ? 2 * N : N;
+  auto wrow_of = [&](int i) -> int64_t {
+    const int64_t wr = EPI == EPI_SWIGLU
+                           ? (int64_t)nb * 64 + r0 + 32 * (i >> 1) + ((i & 1) ? N : 0)
+                           : (int64_t)nb * TN + r0 + 32 * i;
+    return (wr < Nrows ? wr : Nrows - 1) * (K / 8) + unit0;          // in uint4 units
+  };
+  auto xrow_of = [&](int i) -> int64_t {
+    const int64_t xm = m0 + r0 + 32 * i;
+    return (xm < M ? xm : M - 1) * (x_stride / 8) + unit0;
+  };
+  const Src src{reinterpret_cast<const uint4*>(W), reinterpret_cast<const uint4*>(X),
+                wrow_of(0), wrow_of(1), wrow_of(2), wrow_of(3),
+                xrow_of(0), xrow_of(1), xrow_of(2), xrow_of(3)};
+  uint4* lw0 = &sm.w[0][r0 * 8 + (unit0 ^ (r0 & 7))];              // + 256 i: rows + 32 i
+  uint4* lx0 = &sm.x[0][r0 * 8 + (unit0 ^ (r0 & 7))];
+  Stage st0, st1;
+// (the scheduling barrier keeps the loads at the head of the stage: left free, the scheduler
+// moves them behind the contraction and halves the prefetch distance)
+#define QD_LOAD(ST, KS)                                            \
+  {                                                                \
+    load_stage(ST, src, ((KS) < kend ? (KS) : kend - 1) * 8);      \
+    __builtin_amdgcn_sched_barrier(0);                             \
+  }
+#define QD_STORE(ST, BUF) store_stage(ST, lw0 + (BUF) * (TN * 8), lx0 + (BUF) * (TM * 8))
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int fa = (64 * wn + c) * 8, fb = (64 * wm + c) * 8;           // fragment rows (+ 128 t)
+#define QD_COMPUTE(BUF)                                                                        \
+  _Pragma("unroll") for (int s_ = 0; s_ < 2; ++s_) {                                           \
+    const int u_ = (4 * s_ + q) ^ (c & 7);                                                     \
+    uint4 a_[4], b_[4];                                                                        \
+    _Pragma("unroll") for (int t = 0; t < 4; ++t) a_[t] = sm.w[BUF][fa + 128 * t + u_];        \
+    _Pragma("unroll") for (int t = 0; t < 4; ++t) b_[t] = sm.x[BUF][fb + 128 * t + u_];        \
+    _Pragma("unroll") for (int nt = 0; nt < 4; ++nt)                                           \
+    _Pragma("unroll") for (int mt = 0; mt < 4; ++mt)                                           \
+      acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(a_[nt]), as_bf8(b_[mt]),    \
+                                                            acc[nt][mt], 0, 0, 0);             \
+  }
+
+  // Stage s sits in LDS buffer s & 1 while the loads of stage s + 2 are in flight.  The loop
+  // body is a pair of stages with no exit between them (an exit there lets the compiler sink the
+  // first half's loads to their use, behind the contraction they are meant to overlap); an odd
+  // last stage is contracted after the loop.  Loads past the last stage are clamped to it.
+  QD_LOAD(st0, kbeg);
+  QD_LOAD(st1, kbeg + 1);
+  QD_STORE(st0, 0);
+  lds_barrier();
+  int ks = kbeg;
+  for (; ks + 1 < kend; ks += 2) {
+    QD_LOAD(st0, ks + 2);
+    QD_COMPUTE(0);
+    QD_STORE(st1, 1);
+    lds_barrier();
+    QD_LOAD(st1, ks + 3);
+    QD_COMPUTE(1);
+    QD_STORE(st0, 0);
+    lds_barrier();
+  }
+  if (ks < kend) QD_COMPUTE(0);
+#undef QD_LOAD
+#undef QD_STORE
+#undef QD_COMPUTE
+
+  // ---------------------------------------------------------------- epilogue
+  // lane (c, q) of acc[nt][mt] holds rows 4 q + r (r < 4) of the weight tile = output columns
+  // n .. n + 3, for activation row m = m0 + 64 wm + 16 mt + c
+  if constexpr (SPLIT) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int64_t m = m0 + 64 * wm + 16 * mt + c;
+      if (m >= M) continue;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int64_t n = (int64_t)nb * TN + 64 * wn + 16 * nt + 4 * q;
+        *reinterpret_cast<f32x4_t*>(part + ((int64_t)split * M + m) * N + n) = acc[nt][mt];
+      }
+    }
+  } else if constexpr (EPI == EPI_ARGMAX) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int64_t m = m0 + 64 * wm + 16 * mt + c;
+      const bool ok = m < M;
+      float bv = -INFINITY;
+      int32_t bi = 0x7FFFFFFF;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int64_t n = (int64_t)nb * TN + 64 * wn + 16 * nt + 4 * q;
+        if (ok && logits) *reinterpret_cast<f32x4_t*>(logits + m * (int64_t)N + n) = acc[nt][mt];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = rbf(acc[nt][mt][r]);
+          if (v > bv) { bv = v; bi = (int32_t)(n + r); }   // ascending n within the lane
+        }
+      }
+      // across the four q lanes of row c (interleaved column ranges): lowest index on ties
+#pragma unroll
+      for (int sh = 0; sh < 2; ++sh) {
+        const float ov = sh ? lane_xor32(bv) : lane_xor16(bv);
+        const int32_t oi = sh ? __builtin_bit_cast(int32_t, lane_xor32(__builtin_bit_cast(float, bi)))
+                              : __builtin_bit_cast(int32_t, lane_xor16(__builtin_bit_cast(float, bi)));
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      }
+      if (q == 0) {
+        amax_v[wm][wn][16 * mt + c] = bv;
+        amax_i[wm][wn][16 * mt + c] = bi;
+      }
+    }
+    lds_barrier();
+    if (tid < 128) {
+      const int wm2 = tid >> 6, r = tid & 63;
+      const int64_t m = m0 + 64 * wm2 + r;
+      if (m < M) {
+        float bv = amax_v[wm2][0][r];
+        int32_t bi = amax_i[wm2][0][r];
+        const float ov = amax_v[wm2][1][r];
+        const int32_t oi = amax_i[wm2][1][r];
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        pval[m * (int64_t)nblocks + nb] = bv;
+        pidx[m * (int64_t)nblocks + nb] = bi;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int64_t m = m0 + 64 * wm + 16 * mt + c;
+      if (m >= M) continue;
+      if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const int64_t n = (int64_t)nb * 64 + 32 * wn + 16 * nt + 4 * q;
+          float y[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            y[r] = rbf(silu_f(rbf(acc[nt][mt][r]))) * rbf(acc[nt + 2][mt][r]);
+          *reinterpret_cast<uint2*>(out + m * out_stride + n) =
+              make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+        }
+      } else {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          const int64_t n = (int64_t)nb * TN + 64 * wn + 16 * nt + 4 * q;
+          float y[4];
+          if constexpr (EPI == EPI_RES) {
+            const uint2 rv = *reinterpret_cast<const uint2*>(res + m * res_stride + n);
+            y[0] = bflo(rv.x) + rbf(acc[nt][mt][0]);
+            y[1] = bfhi(rv.x) + rbf(acc[nt][mt][1]);
+            y[2] = bflo(rv.y) + rbf(acc[nt][mt][2]);
+            y[3] = bfhi(rv.y) + rbf(acc[nt][mt][3]);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[r] = acc[nt][mt][r];
+          }
+          *reinterpret_cast<uint2*>(out + m * out_stride + n) =
+              make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+        }
+      }
+    }
+  }
+}
+
+// Sum of the split partials in split order + epilogue (store / residual); one thread per four
+// consecutive output columns.
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __restrict__ part,
+                                                                int splits, int64_t M, int64_t N,
+                                                                bf16_t* out, int64_t out_stride,
+                                                                const bf16_t* res,
+                                                                int64_t res_stride) {
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n4 = N / 4;
+  if (g >= M * n4) return;
+  const int64_t m = g / n4, n = 4 * (g % n4);
+  f32x4_t a = *reinterpret_cast<const f32x4_t*>(part + m * N + n);
+  for (int z = 1; z < splits; ++z) a += *reinterpret_cast<const f32x4_t*>(part + ((int64_t)z * M + m) * N + n);
+  float y[4];
+  if constexpr (EPI == EPI_RES) {
+    const uint2 rv = *reinterpret_cast<const uint2*>(res + m * res_stride + n);
+    y[0] = bflo(rv.x) + rbf(a[0]);
+    y[1] = bfhi(rv.x) + rbf(a[1]);
+    y[2] = bflo(rv.y) + rbf(a[2]);
+    y[3] = bfhi(rv.y) + rbf(a[3]);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = a[r];
+  }
+  *reinterpret_cast<uint2*>(out + m * out_stride + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+}
+
+int64_t tile_nblocks(int64_t N, int epi) { return epi == EPI_SWIGLU ? N / 64 : N / TN; }
+
+}  // namespace
+
+bool gemm_tile_ok(int64_t M, int64_t N, int64_t K, int epi, const void* x, int64_t x_stride,
+                  const void* w, const void* out, int64_t out_stride, const void* res,
+                  int64_t res_stride) {
+  if (M <= 0 || K % TK != 0 || K < 2 * TK) return false;
+  if (epi == EPI_SWIGLU ? N % 64 != 0 : N % TN != 0) return false;
+  if (x_stride % 8 || reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w) % 16)
+    return false;
+  if (epi != EPI_ARGMAX && (out_stride % 4 || reinterpret_cast<uintptr_t>(out) % 8)) return false;
+  if (epi == EPI_RES && (res_stride % 4 || reinterpret_cast<uintptr_t>(res) % 8)) return false;
+  return M * (int64_t)(N / 16) < (1ll << 40) && (M + TM - 1) / TM * tile_nblocks(N, epi) < (1ll << 30);
+}
+
+// K splits: only the store / residual epilogues split; enough to put ~256 workgroups in flight,
+// keeping at least 4 stages per split
+int gemm_tile_splits(int64_t M, int64_t N, int64_t K, int epi) {
+  if (epi != EPI_NONE && epi != EPI_RES) return 1;
+  const int64_t tiles = (M + TM - 1) / TM * tile_nblocks(N, epi);
+  if (tiles >= 160) return 1;
+  int64_t sp = (256 + tiles - 1) / tiles;
+  const int64_t maxsp = (K / TK) / 4;
+  if (sp > maxsp) sp = maxsp;
+  return sp < 1 ? 1 : (int)sp;
+}
+
+int64_t gemm_tile_ws_floats(int64_t M, int64_t N, int64_t K, int epi) {
+  const int sp = gemm_tile_splits(M, N, K, epi);
+  return sp > 1 ? (int64_t)sp * M * N : 0;
+}
+
+int64_t gemm_tile_argmax_parts(int64_t N) { return N / TN; }
+
+// Returns the number of argmax partials per row written (EPI_ARGMAX), else 0.
+int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
+                         int64_t K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs, int epi,
+                         float* pval, int32_t* pidx, float* logits, float* part,
+                         int64_t part_floats, hipStream_t s) {
+  const int64_t mblocks = (M + TM - 1) / TM, nblocks = tile_nblocks(N, epi);
+  int splits = gemm_tile_splits(M, N, K, epi);
+  if (splits > 1 && (!part || part_floats < (int64_t)splits * M * N)) splits = 1;
+  const int ksteps = (int)(K / TK);
+  const int ks_per = (ksteps + splits - 1) / splits;
+  splits = (ksteps + ks_per - 1) / ks_per;              // no empty split
+  const dim3 grid((unsigned)(mblocks * nblocks * splits)), block(256);
+  const int Mi = (int)M, Ni = (int)N, Ki = (int)K, mbi = (int)mblocks, nbi = (int)nblocks;
+#define QD_TILE(E, SP)                                                                           \
+  gemm_tile_kernel<E, SP><<<grid, block, 0, s>>>(x, xs, Mi, w, Ni, Ki, mbi, nbi, ks_per, out, os, \
+                                                 res, rs, pval, pidx, logits, part)
+  if (splits > 1) {
+    if (epi == EPI_RES) QD_TILE(EPI_RES, true);
+    else QD_TILE(EPI_NONE, true);
+    const int64_t thr = M * (N / 4);
+    const dim3 rg((unsigned)((thr + 255) / 256));
+    if (epi == EPI_RES)
+      gemm_split_reduce_kernel<EPI_RES><<<rg, block, 0, s>>>(part, splits, M, N, out, os, res, rs);
+    else
+      gemm_split_reduce_kernel<EPI_NONE><<<rg, block, 0, s>>>(part, splits, M, N, out, os, res, rs);
+    return 0;
+  }
+  switch (epi) {
+    case EPI_RES: QD_TILE(EPI_RES, false); break;
+    case EPI_SWIGLU: QD_TILE(EPI_SWIGLU, false); break;
+    case EPI_ARGMAX: QD_TILE(EPI_ARGMAX, false); return nblocks;
+    default: QD_TILE(EPI_NONE, false); break;
+  }
+#undef QD_TILE
+  return 0;
+}

@@ -65,8 +65,9 @@ int lm_head(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t V, int64
     launch_lm_vec(x, x_stride, w, V, K, norm_w, eps, rows, l.val, l.idx, tok, pos_inc, logits, s);
   } else {
     launch_add_rmsnorm(nullptr, x, norm_w, nullptr, l.xn, rows, K, x_stride, K, eps, s);
-    launch_gemm(l.xn, K, rows, w, V, K, nullptr, 0, nullptr, 0, EPI_ARGMAX, l.val, l.idx, logits, s);
-    launch_argmax_reduce(l.val, l.idx, l.parts, rows, tok, pos_inc, s);
+    const int64_t parts = launch_gemm(l.xn, K, rows, w, V, K, nullptr, 0, nullptr, 0, EPI_ARGMAX,
+                                      l.val, l.idx, logits, s);
+    launch_argmax_reduce(l.val, l.idx, parts, rows, tok, pos_inc, s);
   }
   return launched();
 }
@@ -144,10 +145,11 @@ int qd_swiglu(const uint16_t* gu, int64_t gu_stride, uint16_t* out, int64_t out_
   return launched();
 }
 
-int64_t qd_linear_workspace_bytes(int64_t rows, int64_t k, int32_t has_norm) {
-  if (rows <= 0 || k <= 0) return 0;
-  if (gemv_supported(rows, k) || !has_norm) return 0;
-  return align256(rows * k * 2);
+int64_t qd_linear_workspace_bytes(int64_t rows, int64_t n_out, int64_t k, int32_t has_norm) {
+  if (rows <= 0 || n_out <= 0 || k <= 0) return 0;
+  if (gemv_supported(rows, k)) return 0;
+  const int64_t xn = has_norm ? align256(rows * k * 2) : 0;
+  return xn + align256(gemm_tile_ws_floats(rows, n_out, k, QD_EPI_RES) * 4);
 }
 
 int qd_linear(const uint16_t* x, int64_t x_stride, const uint16_t* w, int64_t n_out, int64_t k,
@@ -168,15 +170,20 @@ int qd_linear(const uint16_t* x, int64_t x_stride, const uint16_t* w, int64_t n_
   const bf16_t* xin = x;
   int64_t xin_stride = x_stride;
   if (norm_w) {
-    const int64_t need = qd_linear_workspace_bytes(rows, k, 1);
+    const int64_t need = align256(rows * k * 2);
     if (!workspace || workspace_bytes < need) return QD_EWS;
     bf16_t* xn = static_cast<bf16_t*>(workspace);
     launch_add_rmsnorm(nullptr, x, norm_w, nullptr, xn, rows, k, x_stride, k, eps, s);
     xin = xn;
     xin_stride = k;
   }
+  // the rest of the workspace (if any) takes split-K partials; with too little, K is not split
+  const int64_t used = norm_w ? align256(rows * k * 2) : 0;
+  float* part = workspace && workspace_bytes > used
+                    ? reinterpret_cast<float*>(static_cast<char*>(workspace) + used) : nullptr;
+  const int64_t part_floats = part ? (workspace_bytes - used) / 4 : 0;
   launch_gemm(xin, xin_stride, rows, w, n_out, k, out, out_stride, res, res_stride, epilogue,
-              nullptr, nullptr, nullptr, s);
+              nullptr, nullptr, nullptr, s, part, part_floats);
   return launched();
 }
 
@@ -405,6 +412,17 @@ int qd_mega_step(const qd_weights* w, const qd_decode_state* st, void* stream) {
 }
 
 // ------------------------------------------------------------------ block (tree / prefill chunk)
+// split-K partials of the block step's projections (the largest of qkv, o, down)
+static int64_t block_part_floats(const qd_weights* w, int64_t M) {
+  const int64_t H = w->hidden, QD = (int64_t)w->n_q_heads * 128;
+  int64_t f = gemm_tile_ws_floats(M, qkv_width(w), H, EPI_NONE);
+  const int64_t o = gemm_tile_ws_floats(M, H, QD, EPI_RES);
+  const int64_t d = gemm_tile_ws_floats(M, H, w->inter, EPI_RES);
+  if (o > f) f = o;
+  if (d > f) f = d;
+  return f;
+}
+
 int64_t qd_block_workspace_bytes(const qd_weights* w, int64_t batch, int64_t T, int64_t cap) {
   if (!w || batch <= 0 || T <= 0 || cap <= 0) return 0;
   // LM region first, sized for either row count (all rows or the last row per sequence)
@@ -416,6 +434,7 @@ int64_t qd_block_workspace_bytes(const qd_weights* w, int64_t batch, int64_t T, 
   const int64_t rows = batch * T * w->n_q_heads * block_attn_splits(cap);
   c.take<float>(rows * 128);
   c.take<float>(rows * 2);
+  c.take<float>(block_part_floats(w, batch * T));
   return c.off;
 }
 
@@ -440,6 +459,8 @@ int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
   const int64_t arows = M * Hq * splits;
   float* acc = c.take<float>(arows * 128);
   float* ml = c.take<float>(arows * 2);
+  const int64_t part_floats = block_part_floats(w, M);
+  float* part = c.take<float>(part_floats);
   const int64_t NQKV = qkv_width(w), QD = (int64_t)Hq * 128;
   const int64_t layer_kv = B * Hkv * cap * 128;
 
@@ -452,19 +473,19 @@ int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
     bf16_t* vc = st->v_cache + l * layer_kv;
     launch_add_rmsnorm(nullptr, st->x, w->ln1 + l * H, nullptr, st->xn, M, H, H, H, w->eps, s);
     launch_gemm(st->xn, H, M, w->w_qkv + l * NQKV * H, NQKV, H, st->qkv, NQKV, nullptr, 0, EPI_NONE,
-                nullptr, nullptr, nullptr, s);
+                nullptr, nullptr, nullptr, s, part, part_floats);
     launch_qk_norm_rope(st->qkv, NQKV, w->q_norm + l * 128, w->k_norm + l * 128, st->cos, st->sin,
                         cap, st->base, st->depth, st->causal ? POS_CHUNK : POS_TREE, st->q, kc, vc,
                         B, T, Hq, Hkv, cap, w->eps, s);
     launch_block_attn(st->q, kc, vc, st->base, st->causal ? nullptr : st->anc, B, T, Hq, Hkv, cap,
                       splits, acc, ml, st->attn, s);
     launch_gemm(st->attn, QD, M, w->w_o + l * H * QD, H, QD, st->x, H, st->x, H, EPI_RES, nullptr,
-                nullptr, nullptr, s);
+                nullptr, nullptr, s, part, part_floats);
     launch_add_rmsnorm(nullptr, st->x, w->ln2 + l * H, nullptr, st->xn, M, H, H, H, w->eps, s);
     launch_gemm(st->xn, H, M, w->w_gu + l * 2 * I * H, I, H, st->act, I, nullptr, 0, EPI_SWIGLU,
                 nullptr, nullptr, nullptr, s);
     launch_gemm(st->act, I, M, w->w_down + l * H * I, H, I, st->x, H, st->x, H, EPI_RES, nullptr,
-                nullptr, nullptr, s);
+                nullptr, nullptr, s, part, part_floats);
   }
   if (st->lm_mode == QD_LM_NONE) return launched();
   if (st->lm_mode == QD_LM_LAST)

@@ -47,11 +47,26 @@ void launch_lm_vec(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t V
                    const bf16_t* norm_w, float eps, int64_t M, float* pval, int32_t* pidx,
                    int64_t* tok, int64_t* pos_inc, float* logits, hipStream_t s);
 
-// gemm.hip (MFMA path, any M)
+// gemm.hip (MFMA path, any M).  launch_gemm returns the argmax partials written per row
+// (EPI_ARGMAX; at most gemm_argmax_parts(N)), else 0.  `part` (optional, part_floats floats) is
+// the split-K workspace of the tiled kernel (gemm_tile_ws_floats); without it K is not split.
 int64_t gemm_argmax_parts(int64_t N);
-void launch_gemm(const bf16_t* x, int64_t x_stride, int64_t M, const bf16_t* w, int64_t N,
-                 int64_t K, bf16_t* out, int64_t out_stride, const bf16_t* res, int64_t res_stride,
-                 int epi, float* pval, int32_t* pidx, float* logits, hipStream_t s);
+int64_t launch_gemm(const bf16_t* x, int64_t x_stride, int64_t M, const bf16_t* w, int64_t N,
+                    int64_t K, bf16_t* out, int64_t out_stride, const bf16_t* res,
+                    int64_t res_stride, int epi, float* pval, int32_t* pidx, float* logits,
+                    hipStream_t s, float* part = nullptr, int64_t part_floats = 0);
+// gemm_tile.hip (LDS-tiled MFMA GEMM for M > 64)
+bool gemm_tile_ok(int64_t M, int64_t N, int64_t K, int epi, const void* x, int64_t x_stride,
+                  const void* w, const void* out, int64_t out_stride, const void* res,
+                  int64_t res_stride);
+int gemm_tile_splits(int64_t M, int64_t N, int64_t K, int epi);
+int64_t gemm_tile_ws_floats(int64_t M, int64_t N, int64_t K, int epi);
+int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
+                         int64_t K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs, int epi,
+                         float* pval, int32_t* pidx, float* logits, float* part,
+                         int64_t part_floats, hipStream_t s);
+// rows from which the tiled kernel takes over
+constexpr int64_t GEMM_TILE_MIN_M = 65;
 
 // attn.hip
 // waves per decode-attention unit (4 query heads x 16 keys per wave per iteration)

@@ -60,7 +60,7 @@ SIGNATURES = {
     "qd_qk_norm_rope": ([p, i64, p, p, p, p, i64, p, p, i32, p, p, p, i64, i64, i64, i64, i64,
                          f32, p], i32),
     "qd_swiglu": ([p, i64, p, i64, i64, i64, p], i32),
-    "qd_linear_workspace_bytes": ([i64, i64, i32], i64),
+    "qd_linear_workspace_bytes": ([i64, i64, i64, i32], i64),
     "qd_linear": ([p, i64, p, i64, i64, p, i64, i64, p, f32, i32, p, i64, p, i64, p], i32),
     "qd_lm_head_workspace_bytes": ([i64, i64, i64], i64),
     "qd_lm_head_argmax": ([p, i64, p, i64, i64, i64, p, f32, p, p, p, p, i64, p], i32),

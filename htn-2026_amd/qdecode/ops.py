@@ -143,7 +143,7 @@ def linear(x, w, epilogue=EPI_NONE, norm_w=None, eps=1e-6, res=None, out=None, w
     _check(out, BF16, "out", x.device)
     if res is not None:
         _check(res, BF16, "res", x.device)
-    need = _lib.LIB.qd_linear_workspace_bytes(rows, K, 1 if norm_w is not None else 0)
+    need = _lib.LIB.qd_linear_workspace_bytes(rows, n_out, K, 1 if norm_w is not None else 0)
     if need and ws is None:
         ws = workspace(need, x.device)
     _lib.call("qd_linear", x2.data_ptr(), x2.stride(0), w.data_ptr(), n_out, K, out.data_ptr(),

@@ -75,10 +75,12 @@ int qd_swiglu(const uint16_t *gu, int64_t gu_stride, uint16_t *out, int64_t out_
 
 /* Decode projection out[m, n] = epi(sum_k xin[m, k] W[n, k]) for m < rows, n < n_out, fp32
  * accumulate; xin = RMSNorm(x; norm_w) when norm_w != NULL.  rows <= 2 run the vector-ALU
- * GEMV, more rows the MFMA kernel (which then needs rows*k*2 bytes of workspace for the
- * normalised activations when norm_w != NULL).
- * Replaces Gemv (engine/kernels/gemv.py:161-234) and FastGemm (fast.py:161-213). */
-int64_t qd_linear_workspace_bytes(int64_t rows, int64_t k, int32_t has_norm);
+ * GEMV, more rows the MFMA kernels.  Workspace: rows*k*2 bytes for the normalised activations
+ * when norm_w != NULL (required), then the split-K partials of the tiled kernel (optional: with
+ * less than qd_linear_workspace_bytes, K is not split).
+ * Replaces Gemv (engine/kernels/gemv.py:161-234) and FastGemm (fast.py:161-213); the split-K
+ * partials play the role of the caller-owned partial buffers of gemv.py:189-208. */
+int64_t qd_linear_workspace_bytes(int64_t rows, int64_t n_out, int64_t k, int32_t has_norm);
 int qd_linear(const uint16_t *x, int64_t x_stride, const uint16_t *w, int64_t n_out, int64_t k,
               uint16_t *out, int64_t out_stride, int64_t rows, const uint16_t *norm_w, float eps,
               int32_t epilogue, const uint16_t *res, int64_t res_stride, void *workspace,
