@@ -176,11 +176,31 @@ __device__ __forceinline__ void part_range(int64_t n, int p, int P, int64_t& a, 
   b = n * (p + 1) / P;
 }
 
+// o-projection rows of workgroup wg.  With at least 107 workgroups that run no attention unit
+// and no split merge, those take all of the rows (at most 24 each): an attention workgroup
+// issues its o / gate-up weight loads only after its unit, so o rows there would put its late
+// weight stream on the critical path of the MID hand-off.  Otherwise all workgroups share them.
+__device__ __forceinline__ void o_rows(const MegaParams& p, int wg, int P, int64_t& a, int64_t& b) {
+  const int units = HKV * p.splits;
+  const int nmerge = p.splits > 1 ? HQ : 0;
+  const int nfree = P - units - nmerge;
+  if (nfree >= 107) {
+    const int f = wg - units;
+    if (f >= 0 && f < nfree) {
+      part_range(H / 2, f, nfree, a, b);
+    } else {
+      a = b = 0;
+    }
+  } else {
+    part_range(H / 2, wg, P, a, b);
+  }
+}
+
 struct Smem {
   uint4 xs[INTER / 8];             // the phase's input row (bf16), up to 9728 values
   float red[16];
   uint16_t obuf[64];               // the workgroup's outputs of the phase, in row order
-  float rown[16];                  // residual values of the workgroup's o / down rows
+  float rown[32];                  // residual values of the workgroup's o / down rows
   float best_v[MG_NW];
   int32_t best_i[MG_NW];
   DecodeAttnLds<ATTN_NW> attn;
@@ -222,7 +242,7 @@ __device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, u
   lds_barrier();
   {                                // residual values of this workgroup's o rows
     int64_t oa, ob;
-    part_range(H / 2, wg, P, oa, ob);
+    o_rows(p, wg, P, oa, ob);
     const int t = threadIdx.x;
     if (t < 2 * (ob - oa)) sm.rown[t] = bf2f(reinterpret_cast<const bf16_t*>(sm.xs)[2 * oa + t]);
   }
@@ -329,17 +349,19 @@ __device__ void phase_merge(const MegaParams& p, int l, int hq, uint32_t tag) {
   ll_put(LL + ly.att + (int64_t)hq * (HD / 2) + lane, pack2(y.x, y.y), tag);
 }
 
-// mid = x + bf16(attn . Wo^T)   (10 rows: waves 0..7, waves 0, 1 take a second row), then
+// mid = x + bf16(attn . Wo^T)   (the workgroup's o rows, o_rows: row wave + 8 rr), then
 // act = bf16(silu(bf16(g))) * bf16(u), g / u = RMSNorm(mid; ln2) . Wgate / Wup^T (act rows
 // wave + 8 rr of the workgroup's 38).  The first two act rows' gate/up weights are loaded
 // together with the o rows, before the attention output is awaited, so they stream during the
-// attention hand-offs; later act rows are double-buffered.
+// attention hand-offs; the third after the o rows are consumed, so it streams during the MID
+// hand-off; later act rows refill the 3-slot ring as rows are consumed.  A workgroup without o
+// rows skips the attention output and goes straight to the MID wait.
 __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t tag) {
   const int wave = threadIdx.x >> 6;
   const Layout ly = ll_layout(p.L, p.splits);
   uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
   int64_t a, b;
-  part_range(H / 2, wg, P, a, b);
+  o_rows(p, wg, P, a, b);
   const int64_t r0 = 2 * a;
   const int nr = (int)(2 * (b - a));
   int64_t ga, gb;
@@ -349,48 +371,52 @@ __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, 
   const bf16_t* W = p.w_o + (int64_t)l * H * (HQ * HD);
   const bf16_t* WG = p.w_gu + (int64_t)l * 2 * INTER * H;
   constexpr int RW = 5;            // act rows per wave (<= 38 per workgroup)
-  uint4 w[2][8], g[2][5], u[2][5];
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr)
-    if (wave + rr * MG_NW < nr) mg_load_row<8>(W, r0 + wave + rr * MG_NW, w[rr]);
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    if (wave + rr * MG_NW < ng) {
-      mg_load_row<5>(WG, g0 + wave + rr * MG_NW, g[rr]);
-      mg_load_row<5>(WG, g0 + wave + rr * MG_NW + INTER, u[rr]);
-    }
-  }
-  ll_fetch_lds<4>(LL + ly.att, HQ * HD / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
-  lds_barrier();
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
+  uint4 w[3][8], g[3][5], u[3][5];  // o rows; a 3-slot ring of act rows (gate, up)
+  auto load_gu = [&](int slot, int rr) {
     const int k = wave + rr * MG_NW;
-    if (k < nr) {
-      const float acc = mg_dot<8>(w[rr], sm.xs);
-      if ((threadIdx.x & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(sm.rown[k] + rbf(acc));
+    if (k < ng) {
+      mg_load_row<5>(WG, g0 + k, g[slot]);
+      mg_load_row<5>(WG, g0 + k + INTER, u[slot]);
     }
+  };
+#pragma unroll
+  for (int rr = 0; rr < 3; ++rr)
+    if (wave + rr * MG_NW < nr) mg_load_row<8>(W, r0 + wave + rr * MG_NW, w[rr]);
+  load_gu(0, 0);
+  load_gu(1, 1);
+  if (nr > 0) {                    // uniform over the workgroup
+    ll_fetch_lds<4>(LL + ly.att, HQ * HD / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
+    lds_barrier();
+#pragma unroll
+    for (int rr = 0; rr < 3; ++rr) {
+      const int k = wave + rr * MG_NW;
+      if (k < nr) {
+        const float acc = mg_dot<8>(w[rr], sm.xs);
+        if ((threadIdx.x & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(sm.rown[k] + rbf(acc));
+      }
+    }
+    lds_barrier();
+    put_pairs(sm, LL + ly.mid, a, nr, tag);
   }
-  lds_barrier();
-  put_pairs(sm, LL + ly.mid, a, nr, tag);
+  load_gu(2, 2);                   // streams during the MID hand-off
   // ---- gate/up + SwiGLU
   ll_fetch_lds<3>(LL + ly.mid, H / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
   lds_barrier();
   {                                // residual values of this workgroup's down rows
+    int64_t da, db;
+    part_range(H / 2, wg, P, da, db);
     const int t = threadIdx.x;
-    if (t < nr) sm.rown[t] = bf2f(reinterpret_cast<const bf16_t*>(sm.xs)[r0 + t]);
+    if (t < 2 * (db - da))
+      sm.rown[t] = bf2f(reinterpret_cast<const bf16_t*>(sm.xs)[2 * da + t]);
   }
   mg_norm<5, 512>(sm.xs, p.ln2 + (int64_t)l * H, p.eps, sm.red);
 #pragma unroll
   for (int rr = 0; rr < RW; ++rr) {
     const int k = wave + rr * MG_NW;
     if (k < ng) {
-      const float ag = mg_dot<5>(g[rr & 1], sm.xs);
-      const float au = mg_dot<5>(u[rr & 1], sm.xs);
-      const int kn = k + 2 * MG_NW;
-      if (rr + 2 < RW && kn < ng) {
-        mg_load_row<5>(WG, g0 + kn, g[rr & 1]);
-        mg_load_row<5>(WG, g0 + kn + INTER, u[rr & 1]);
-      }
+      const float ag = mg_dot<5>(g[rr % 3], sm.xs);
+      const float au = mg_dot<5>(u[rr % 3], sm.xs);
+      if (rr + 3 < RW) load_gu(rr % 3, rr + 3);
       if ((threadIdx.x & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(rbf(silu_f(rbf(ag))) * rbf(au));
     }
   }
