@@ -149,11 +149,20 @@ __device__ __forceinline__ float mg_dot(const uint4* wv, const uint4* xs) {
   return wave_sum(a);
 }
 
+// The thread's chunk of an RMSNorm weight vector (chunk threadIdx.x of KCH * 64), loaded when
+// a phase starts so that the norm after the input's hand-off does not wait on it.
+template <int KCH>
+__device__ __forceinline__ uint4 mg_norm_w(const bf16_t* __restrict__ norm_w) {
+  static_assert(KCH * 64 <= MG_NT, "one chunk per thread");
+  const int tid = threadIdx.x;
+  return tid < KCH * 64 ? reinterpret_cast<const uint4*>(norm_w)[tid] : make_uint4(0, 0, 0, 0);
+}
+
 // RMSNorm of the raw row in xs (in place), statistics over VNT virtual threads exactly as a
-// VNT-thread workgroup of gemv_kernel / lm_vec_kernel computes them (VNT in {256, 512}).
+// VNT-thread workgroup of gemv_kernel / lm_vec_kernel computes them (VNT in {256, 512}); nw is
+// the thread's weight chunk (mg_norm_w).
 template <int KCH, int VNT>
-__device__ __forceinline__ void mg_norm(uint4* xs, const bf16_t* __restrict__ norm_w, float eps,
-                                        float* red) {
+__device__ __forceinline__ void mg_norm(uint4* xs, uint4 nw, float eps, float* red) {
   constexpr int NCH = KCH * 64;
   static_assert(VNT == 256 || VNT == 512, "virtual thread count");
   const int tid = threadIdx.x;
@@ -166,8 +175,7 @@ __device__ __forceinline__ void mg_norm(uint4* xs, const bf16_t* __restrict__ no
   float tot = 0.f;
   for (int q = 0; q < VNT / 64; ++q) tot += red[q];
   const float rstd = rstd_of(tot, KCH * 512, eps);
-  const uint4* wr = reinterpret_cast<const uint4*>(norm_w);
-  for (int c = tid; c < NCH; c += MG_NT) xs[c] = norm8(xs[c], wr[c], rstd);
+  if (tid < NCH) xs[tid] = norm8(xs[tid], nw, rstd);
   lds_barrier();
 }
 
@@ -230,6 +238,7 @@ __device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, u
 #pragma unroll
   for (int rr = 0; rr < 3; ++rr)
     if (wave + rr * MG_NW < nr) mg_load_row<5>(W, r0 + wave + rr * MG_NW, w[rr]);
+  const uint4 nw = mg_norm_w<5>(p.ln1 + (int64_t)l * H);
   uint32_t* xs32 = reinterpret_cast<uint32_t*>(sm.xs);
   if (l == 0) {                    // the embedding row (an id outside the vocab reads zeros)
     const bool ok = tok >= 0 && tok < p.vocab;
@@ -246,7 +255,7 @@ __device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, u
     const int t = threadIdx.x;
     if (t < 2 * (ob - oa)) sm.rown[t] = bf2f(reinterpret_cast<const bf16_t*>(sm.xs)[2 * oa + t]);
   }
-  mg_norm<5, 512>(sm.xs, p.ln1 + (int64_t)l * H, p.eps, sm.red);
+  mg_norm<5, 512>(sm.xs, nw, p.eps, sm.red);
 #pragma unroll
   for (int rr = 0; rr < 3; ++rr) {
     const int k = wave + rr * MG_NW;
@@ -399,6 +408,7 @@ __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, 
     put_pairs(sm, LL + ly.mid, a, nr, tag);
   }
   load_gu(2, 2);                   // streams during the MID hand-off
+  const uint4 nw = mg_norm_w<5>(p.ln2 + (int64_t)l * H);
   // ---- gate/up + SwiGLU
   ll_fetch_lds<3>(LL + ly.mid, H / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
   lds_barrier();
@@ -409,7 +419,7 @@ __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, 
     if (t < 2 * (db - da))
       sm.rown[t] = bf2f(reinterpret_cast<const bf16_t*>(sm.xs)[2 * da + t]);
   }
-  mg_norm<5, 512>(sm.xs, p.ln2 + (int64_t)l * H, p.eps, sm.red);
+  mg_norm<5, 512>(sm.xs, nw, p.eps, sm.red);
 #pragma unroll
   for (int rr = 0; rr < RW; ++rr) {
     const int k = wave + rr * MG_NW;
@@ -465,10 +475,11 @@ __device__ void phase_lm(const MegaParams& p, Smem& sm, int wg, int P, uint32_t 
 #pragma unroll
   for (int s = 0; s < 4; ++s)
     if (wave + s * MG_NW < nr) mg_load_row<5>(p.embed, r0 + wave + s * MG_NW, buf[s]);
+  const uint4 nw = mg_norm_w<5>(p.final_norm);
   const uint64_t* last = p.ll + (int64_t)(p.L - 1) * ly.per_layer + ly.out;
   ll_fetch_lds<3>(last, H / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
   lds_barrier();
-  mg_norm<5, 256>(sm.xs, p.final_norm, p.eps, sm.red);
+  mg_norm<5, 256>(sm.xs, nw, p.eps, sm.red);
   float bv = -INFINITY;
   int32_t bi = 0x7FFFFFFF;
   for (int k0 = wave; k0 < nr; k0 += 4 * MG_NW) {
