@@ -18,16 +18,24 @@ transformers model, no torch compute and no fallback tier -- a missing library r
 import gc
 import os
 import sys
+import time
 
 import torch
 
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 
 from qdecode import _lib  # noqa: E402
+from qdecode import draft as _draft  # noqa: E402
 from qdecode import model as _model  # noqa: E402
 from qdecode import tree as _tree  # noqa: E402
 
 DEVICE = os.environ.get("ENGINE_DEVICE", "cuda:0")
+# Tree speculation in generate() (engine.py:87, 910-936): "auto" decides per shape on its first
+# call (the reference's warmup gate), "1" always, "0" never.
+TREE_MODE = os.environ.get("ENGINE_TREE", "auto")
+TREE_CHECK_TOKENS = 128   # tokens the gate generates each way (engine.py:88)
+TREE_MIN_GAIN = 0.92      # keep trees only below this fraction of the plain wall time (engine.py:89)
+TREE_MAX_ROWS = 64        # verification rows B * T: the weight-streaming GEMM regime
 
 
 class _Shape:
@@ -89,11 +97,16 @@ class Engine:
         self.tree_T = int(os.environ.get("ENGINE_TREE_T", "0"))
         self.prefill_budget_rows = None    # rows per causal prefill chunk (None: 4096)
         self.tree_stats = None
+        self.tree_mode = TREE_MODE
+        self.tree_on = {}                  # (B, S, N) -> the gate's decision
+        self.tree_log = {}                 # (B, S, N) -> what the gate measured
 
     # -------------------------------------------------------------- state
-    def _state(self, B, S, N):
+    def _state(self, B, S, N, tree_T=None):
+        """Buffers for (B, S, N) with a tree runner of tree_T nodes (default self.tree_T)."""
+        tree_T = self.tree_T if tree_T is None else tree_T
         sh = self.shape
-        if sh is not None and (sh.B, sh.S, sh.N) == (B, S, N):
+        if sh is not None and (sh.B, sh.S, sh.N, sh.tree_T) == (B, S, N, tree_T):
             return sh
         if sh is not None:
             sh.decode.close()
@@ -101,7 +114,7 @@ class Engine:
         gc.collect()
         torch.cuda.empty_cache()
         with torch.cuda.stream(self.stream):
-            sh = _Shape(self.model, self.stream, B, S, N, self.tree_T, self.prefill_budget_rows)
+            sh = _Shape(self.model, self.stream, B, S, N, tree_T, self.prefill_budget_rows)
         self.stream.synchronize()
         self.shape = sh
         return sh
@@ -125,14 +138,52 @@ class Engine:
             return
         ids = self._check_ids(input_ids, self.model.V)
         B, S = ids.shape
+        T = self._tree_width(B, N)
         gc_was = gc.isenabled()
         gc.disable()
         try:
-            sh = self._state(B, S, N)
-            yield from self._stream_plain(sh, ids, N)
+            sh = self._state(B, S, N, T)
+            key = (B, S, N)
+            if T and key not in self.tree_on:
+                self.tree_on[key] = (self.tree_mode == "1" or
+                                     self._decide_tree(sh, ids, min(N, TREE_CHECK_TOKENS)))
+            if T and self.tree_on[key]:
+                yield from _tree.stream_tree(self, sh, ids, N, _draft.LookaheadDrafter())
+            else:
+                yield from self._stream_plain(sh, ids, N)
         finally:
             if gc_was:
                 gc.enable()
+
+    def _tree_width(self, B, N):
+        """Verification tree size for tree speculation in generate() (0: off): as many nodes as
+        keep B * T within TREE_MAX_ROWS, between 8 and 64 (the ancestor mask is 64 bits)."""
+        if self.tree_mode == "0" or N <= 1 or B * 8 > TREE_MAX_ROWS:
+            return 0
+        return min(64, TREE_MAX_ROWS // B)
+
+    def _decide_tree(self, sh, ids, n):
+        """The warmup gate (engine.py:910-936): n tokens with tree speculation and n plain on
+        the same buffers; keep trees only if they emit exactly the plain greedy ids and take
+        less than TREE_MIN_GAIN of the plain wall time (best of two runs each)."""
+        def run(tree):
+            t0 = time.perf_counter()
+            it = (_tree.stream_tree(self, sh, ids, n, _draft.LookaheadDrafter()) if tree
+                  else self._stream_plain(sh, ids, n))
+            out = list(it)
+            return out, time.perf_counter() - t0
+        plain, _ = run(False)
+        tree, _ = run(True)
+        exact = tree == plain
+        ms_tree = min(run(True)[1] for _ in range(2)) * 1e3
+        ms_plain = min(run(False)[1] for _ in range(2)) * 1e3
+        on = exact and ms_tree < TREE_MIN_GAIN * ms_plain
+        stats = self.tree_stats or {}
+        acc = stats.get("accepted") or [1]
+        self.tree_log[(sh.B, sh.S, sh.N)] = {
+            "tokens": n, "exact": exact, "tree_ms": round(ms_tree, 3), "plain_ms": round(ms_plain, 3),
+            "accept_mean": round(sum(acc) / len(acc), 3), "T": sh.tree_T, "on": on}
+        return on
 
     def _stream_plain(self, sh, ids, N):
         """Prefill, then N-1 graph replays of the decode step; the host yields step t-1 while
@@ -173,21 +224,17 @@ class Engine:
                                "QD_MEGA=0 selects the per-launch step")
 
     # -------------------------------------------------------------- tree speculation
-    def generate_tree(self, input_ids, max_new_tokens, drafter, T=64):
+    def generate_tree(self, input_ids, max_new_tokens, drafter=None, T=64):
         """Exact token-tree speculative decoding (engine.py:830-908): every step verifies a
         T-node draft tree per sequence in one block forward and emits the longest
-        greedy-matching path.  ``drafter(seq, T) -> _tree.Tree`` supplies the drafts."""
+        greedy-matching path.  ``drafter``: ``draft.LookaheadDrafter`` (the default: window,
+        n-gram and prediction-pool sources) or any ``drafter(seq, T) -> tree.Tree``."""
         N = int(max_new_tokens)
         if N <= 0:
             return
         ids = self._check_ids(input_ids, self.model.V)
         B, S = ids.shape
-        old_T = self.tree_T
-        self.tree_T = T
-        try:
-            if self.shape is None or self.shape.tree_T != T or (self.shape.B, self.shape.S, self.shape.N) != (B, S, N):
-                self.shape = None
-            sh = self._state(B, S, N)
-        finally:
-            self.tree_T = old_T
-        yield from _tree.stream_tree(self, sh, ids, N, drafter)
+        if not 2 <= T <= 64:
+            raise ValueError("T must lie in [2, 64] (64-bit ancestor masks)")
+        sh = self._state(B, S, N, T)
+        yield from _tree.stream_tree(self, sh, ids, N, drafter or _draft.LookaheadDrafter())

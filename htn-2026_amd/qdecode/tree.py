@@ -5,7 +5,9 @@ its verify loop (engine/engine.py:830-908) with two MI355X-side changes:
   * the ancestor-or-self mask is 64 bits wide (the reference's int32 caps trees at 32 nodes,
     engine.py:166-169), so a 64-node tree verifies in one block forward;
   * draft sources are pluggable: ``random_tree_drafter`` builds the benchmark's uniformly
-    random 4-4-2-2 trees; the reference's n-gram / Jacobi sources are not part of this path.
+    random 4-4-2-2 trees; ``draft.LookaheadDrafter`` restates the reference's window / n-gram
+    / prediction-pool sources (a stateful drafter: ``rows(seqs)`` gives per-sequence sources
+    that draft a tree, observe the verified argmaxes and index the emitted text).
 
 Node 0 is the last emitted token (its K/V is not cached yet); parents precede children, so
 node index >= depth.  Node i is rotated at base + depth_i, written to cache slot base + i,
@@ -134,6 +136,8 @@ def stream_tree(engine, sh, ids, N, drafter):
     if N == 1:
         return
     seqs = [list(map(int, r)) + [t] for r, t in zip(ids.tolist(), first)]
+    rows = drafter.rows(seqs) if hasattr(drafter, "rows") else None
+    depth = min(T - 1, getattr(drafter, "max_depth", T - 1))
     c_base, c_src, c_cnt = [S] * B, [[0] * T for _ in range(B)], [1] * B
     pin = lambda shape, dt: torch.empty(shape, dtype=dt, pin_memory=True)  # noqa: E731
     h_tok, h_depth, h_anc = pin((B, T), torch.int64), pin((B, T), torch.int64), pin((B, T), torch.int64)
@@ -153,7 +157,7 @@ def stream_tree(engine, sh, ids, N, drafter):
                 trees.append(None)
                 bases.append(S)
             else:
-                tree = drafter(sq, T)
+                tree = rows[b].draft(T, depth) if rows else drafter(sq, T)
                 trees.append(tree)
                 bases.append(len(sq) - 1)
             h_tok[b] = torch.tensor(tree.tokens, dtype=torch.int64)
@@ -177,11 +181,16 @@ def stream_tree(engine, sh, ids, N, drafter):
             if tree is None:
                 c_cnt[b] = 1
                 continue
-            emitted, path = accept(tree, g[b * T:(b + 1) * T])
+            gb = g[b * T:(b + 1) * T]
+            emitted, path = accept(tree, gb)
             c_base[b] = bases[b]
             c_src[b] = [0] + path + [0] * (T - 1 - len(path))
             c_cnt[b] = len(path) + 1
+            if rows:
+                rows[b].observe(tree, gb, path)
             seqs[b].extend(emitted)
+            if rows:
+                rows[b].index()
             stats["accepted"].append(len(emitted))
         while yielded < N and all(len(sq) - S > yielded for sq in seqs):
             yield [sq[S + yielded] for sq in seqs]

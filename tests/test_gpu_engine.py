@@ -190,6 +190,32 @@ def test_tree_random_drafts_config5_shape(eng2, ref2):
     assert margin_rule(got, tl, margin=ORACLE_TIE) == []
 
 
+def test_generate_tree_modes(eng2, ref2):
+    """generate() with tree speculation forced on (the lookahead / n-gram / pool drafter) emits
+    greedy ids under the margin rule; the warmup gate decides once per shape, records what it
+    measured, and either way returns the plain greedy ids of its own check."""
+    say("generate: ENGINE_TREE=1 (lookahead drafts), then the auto gate, B=2 S=48 N=24")
+    prompt = synth.prompt_ids(41, 2, 48)
+    mode = eng2.tree_mode
+    try:
+        eng2.tree_mode = "0"
+        plain = np.array(list(eng2.generate(prompt.tolist(), 24))).T
+        eng2.tree_mode, eng2.tree_on = "1", {}
+        tree = np.array(list(eng2.generate(prompt.tolist(), 24))).T
+        assert eng2.tree_stats["passes"] >= 1 and sum(eng2.tree_stats["accepted"]) >= 23
+        tl = ref2.teacher_logits(prompt, tree)
+        assert margin_rule(tree, tl, margin=ORACLE_TIE) == []
+        eng2.tree_mode, eng2.tree_on = "auto", {}
+        auto = np.array(list(eng2.generate(prompt.tolist(), 24))).T
+        log = eng2.tree_log[(2, 48, 24)]
+        print(f"gate: {log}", flush=True)
+        assert log["T"] == 32 and log["tokens"] == 24 and log["on"] == eng2.tree_on[(2, 48, 24)]
+        assert log["on"] <= log["exact"]
+        assert np.array_equal(auto, plain) or (log["on"] and np.array_equal(auto, tree))
+    finally:
+        eng2.tree_mode, eng2.tree_on = mode, {}
+
+
 def test_checkpoint_engine_matches_synthetic(Engine, tmp_path):
     say("Engine(model_path) on a written 1-layer checkpoint == Engine.synthetic")
     ensure_oracle_built()
