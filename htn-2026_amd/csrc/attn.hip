@@ -138,67 +138,10 @@ void launch_decode_attn(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn,
 // ------------------------------------------------------------------ block (tree / causal chunk)
 constexpr int64_t BLOCK_CHUNK = 512;
 
-__global__ __launch_bounds__(256) void block_attn_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
-    const bf16_t* __restrict__ v_cache, const int64_t* __restrict__ base_ptr,
-    const uint64_t* __restrict__ anc, int64_t T, int Hq, int Hkv, int64_t cap, float scale,
-    float* ws_acc, float* ws_ml) {
-  const int split = blockIdx.x, kvh = blockIdx.y;
-  const int splits = gridDim.x;
-  const int64_t TQ = (T + 3) / 4;
-  const int64_t b = blockIdx.z / TQ;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t t = (blockIdx.z % TQ) * 4 + wave;
-  if (t >= T) return;  // no barrier below: waves are independent
-  const int g = lane >> 4, i = lane & 15;
-  const int64_t base = base_ptr[b];
-  const uint64_t mask = anc ? anc[b * T + t] : 0;
-  float qv[GRP][8];
-  const uint4* qr = reinterpret_cast<const uint4*>(q + ((b * T + t) * Hq + kvh * GRP) * 128);
-#pragma unroll
-  for (int h = 0; h < GRP; ++h) unpack8(qr[h * 16 + i], qv[h]);
-  SoftmaxState st;
-  state_init(st);
-  const int64_t start = (int64_t)split * BLOCK_CHUNK;
-  int64_t kend = start + BLOCK_CHUNK;
-  if (kend > base + T) kend = base + T;
-  if (kend > cap) kend = cap;
-  const int64_t head_off = ((b * Hkv + kvh) * cap) * 128;
-  const uint4* kb = reinterpret_cast<const uint4*>(k_cache + head_off);
-  const uint4* vb = reinterpret_cast<const uint4*>(v_cache + head_off);
-  for (int64_t j0 = start; j0 < kend; j0 += GRP * KPG) {
-    float kf[KPG][8], vf[KPG][8], s[KPG][GRP];
-    bool ok[KPG];
-#pragma unroll
-    for (int kk = 0; kk < KPG; ++kk) {
-      const int64_t j = j0 + g * KPG + kk;
-      bool vis = j < kend;
-      if (vis && j >= base) {
-        const int64_t jb = j - base;
-        vis = anc ? ((mask >> jb) & 1ull) != 0 : jb <= t;
-      }
-      ok[kk] = vis;
-      const int64_t jj = j < kend ? j : start;
-      unpack8(kb[jj * 16 + i], kf[kk]);
-      unpack8(vb[jj * 16 + i], vf[kk]);
-    }
-    group_scores(qv, kf, ok, scale, s);
-    state_update(st, s, vf);
-  }
-  state_merge_xor(st, 16);
-  state_merge_xor(st, 32);
-  if (lane < 16) {
-#pragma unroll
-    for (int h = 0; h < GRP; ++h) {
-      const int64_t idx = (((b * T + t) * Hq + kvh * GRP + h) * splits + split);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ws_acc[idx * 128 + 8 * i + e] = st.acc[h][e];
-      if (i == 0) { ws_ml[idx * 2] = st.m[h]; ws_ml[idx * 2 + 1] = st.l[h]; }
-    }
-  }
-}
-
-// MFMA version (v_mfma_f32_16x16x32_bf16).  Workgroup = (key split of BLOCK_CHUNK keys, KV
+// Block attention for T query tokens per sequence (tree verification with ancestor masks, causal
+// prefill chunks): query token t of sequence b sees every cached key < base[b] and block key
+// base[b] + j iff bit j of anc[b*T + t] (tree.py:72-195, engine.py:445-461) or j <= t (causal).
+// v_mfma_f32_16x16x32_bf16.  Workgroup = (key split of BLOCK_CHUNK keys, KV
 // head, block of BA_TQ query tokens of one sequence); wave w handles query head kvh*4 + w for the
 // block's tokens (two 16-row tiles).  Keys go in tiles of 32:
 //  * S' = K . Q^T: A = K tile rows (LDS, 16-byte units XOR-swizzled by key), B = the lane's query
@@ -211,7 +154,8 @@ __global__ __launch_bounds__(256) void block_attn_kernel(
 //    by both operands), so O^T's lane (c, q) holds dims 16 dt + 4q..+3 of row c and the per-row
 //    rescale needs no cross-lane traffic;
 //  * the next key tile is loaded into registers while the current one is consumed.
-// Writes (m, l, acc) partials per (row, split) like block_attn_kernel; attn_merge_kernel merges.
+// Writes (m, l, acc) partials per (query row, head, split) -- ws_acc[idx * 128 + d], ws_ml[idx * 2],
+// idx = ((b*T + t)*Hq + h)*splits + split -- which attn_merge_kernel merges.
 constexpr int BA_TQ = 32;
 constexpr int BA_VT = 36;  // V^T row stride (bf16): 72 bytes, 16 rows hit 32 distinct banks
 
