@@ -141,9 +141,10 @@ constexpr int64_t BLOCK_CHUNK = 512;
 // Block attention for T query tokens per sequence (tree verification with ancestor masks, causal
 // prefill chunks): query token t of sequence b sees every cached key < base[b] and block key
 // base[b] + j iff bit j of anc[b*T + t] (tree.py:72-195, engine.py:445-461) or j <= t (causal).
-// v_mfma_f32_16x16x32_bf16.  Workgroup = (key split of BLOCK_CHUNK keys, KV
-// head, block of BA_TQ query tokens of one sequence); wave w handles query head kvh*4 + w for the
-// block's tokens (two 16-row tiles).  Keys go in tiles of 32:
+// v_mfma_f32_16x16x32_bf16.  Workgroup = (key split of BLOCK_CHUNK keys, KV head, block of
+// BA_TQ = 64 query tokens of one sequence), 8 waves: wave w handles query head kvh*4 + (w & 3)
+// for the block's tokens 32 (w >> 2) .. + 31 (two 16-row tiles), so every staged K/V tile
+// serves 64 tokens x 4 heads.  Keys go in tiles of 32:
 //  * S' = K . Q^T: A = K tile rows (LDS, 16-byte units XOR-swizzled by key), B = the lane's query
 //    row (registers); lane (c, q) ends up holding the scores of its query row c against keys
 //    4q..4q+3 and 16+4q..16+4q+3 of the tile;
@@ -153,13 +154,14 @@ constexpr int64_t BLOCK_CHUNK = 512;
 //    8 probabilities, taken in that same key order (a permutation of the contraction index shared
 //    by both operands), so O^T's lane (c, q) holds dims 16 dt + 4q..+3 of row c and the per-row
 //    rescale needs no cross-lane traffic;
-//  * the next key tile is loaded into registers while the current one is consumed.
+//  * staging: thread i moves K and V unit i % 16 of key i / 16 of a tile; the next three tiles'
+//    loads are in flight (a register ring) while a tile is staged and contracted.
 // Writes (m, l, acc) partials per (query row, head, split) -- ws_acc[idx * 128 + d], ws_ml[idx * 2],
 // idx = ((b*T + t)*Hq + h)*splits + split -- which attn_merge_kernel merges.
-constexpr int BA_TQ = 32;
+constexpr int BA_TQ = 64;
 constexpr int BA_VT = 36;  // V^T row stride (bf16): 72 bytes, 16 rows hit 32 distinct banks
 
-__global__ __launch_bounds__(256) void block_attn_mfma_kernel(
+__global__ __launch_bounds__(512) void block_attn_mfma_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
     const bf16_t* __restrict__ v_cache, const int64_t* __restrict__ base_ptr,
     const uint64_t* __restrict__ anc, int64_t T, int Hq, int Hkv, int64_t cap, float scale,
@@ -172,11 +174,13 @@ __global__ __launch_bounds__(256) void block_attn_mfma_kernel(
   const int splits = gridDim.x;
   const int64_t QB = (T + BA_TQ - 1) / BA_TQ;
   const int64_t b = blockIdx.z / QB;
-  const int64_t t0 = (blockIdx.z % QB) * BA_TQ;
+  const int64_t tb = (blockIdx.z % QB) * BA_TQ;             // the workgroup's first token
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int head = wave & 3;
+  const int64_t t0 = tb + 32 * (wave >> 2);                 // this wave's first token
   const int c = lane & 15, q4 = lane >> 4;
   const int64_t base = base_ptr[b];
-  // query rows of this lane: token t0 + 16 rt + c, head kvh * 4 + wave
+  // query rows of this lane: token t0 + 16 rt + c, head kvh * 4 + head
   uint4 qf[2][4];
   uint64_t mask[2];
   int64_t tok[2];
@@ -184,7 +188,7 @@ __global__ __launch_bounds__(256) void block_attn_mfma_kernel(
   for (int rt = 0; rt < 2; ++rt) {
     tok[rt] = t0 + 16 * rt + c;
     const int64_t tt = tok[rt] < T ? tok[rt] : T - 1;
-    const uint4* qr = reinterpret_cast<const uint4*>(q + ((b * T + tt) * Hq + kvh * GRP + wave) * 128);
+    const uint4* qr = reinterpret_cast<const uint4*>(q + ((b * T + tt) * Hq + kvh * GRP + head) * 128);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) qf[rt][kk] = qr[4 * kk + q4];
     mask[rt] = anc ? anc[b * T + tt] : 0;
@@ -192,8 +196,9 @@ __global__ __launch_bounds__(256) void block_attn_mfma_kernel(
   const int64_t start = (int64_t)split * BLOCK_CHUNK;
   int64_t kend = start + BLOCK_CHUNK;
   if (kend > base + T) kend = base + T;
-  if (!anc && kend > base + t0 + BA_TQ) kend = base + t0 + BA_TQ;   // causal: later keys unseen
+  if (!anc && kend > base + tb + BA_TQ) kend = base + tb + BA_TQ;   // causal: later keys unseen
   if (kend > cap) kend = cap;
+  const int ntiles = kend > start ? (int)((kend - start + 31) / 32) : 0;
   const int64_t head_off = ((b * Hkv + kvh) * cap) * 128;
   const uint4* kb = reinterpret_cast<const uint4*>(k_cache + head_off);
   const uint4* vb = reinterpret_cast<const uint4*>(v_cache + head_off);
@@ -203,38 +208,24 @@ __global__ __launch_bounds__(256) void block_attn_mfma_kernel(
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) o[rt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // staging: thread tid moves units 2 tid, 2 tid + 1 of the 32 x 16-unit K and V tiles (key
-  // tid / 8, units 2 (tid % 8) and 2 (tid % 8) + 1)
-  const int skey = tid >> 3, su = 2 * (tid & 7);
-  uint4 kx0, kx1, vx0, vx1;
-  {
-    const int64_t j = start + skey < cap ? start + skey : cap - 1;
-    kx0 = kb[j * 16 + su]; kx1 = kb[j * 16 + su + 1];
-    vx0 = vb[j * 16 + su]; vx1 = vb[j * 16 + su + 1];
+  const int skey = tid >> 4, su = tid & 15;
+  // load tile `it` (clamped into the cache: tiles past the range reload valid keys, unused)
+#define BA_LD(IT, KX, VX)                                                      \
+  {                                                                            \
+    const int64_t jn_ = start + 32 * (int64_t)(IT) + skey;                     \
+    const int64_t j_ = jn_ < cap ? jn_ : cap - 1;                              \
+    KX = kb[j_ * 16 + su];                                                     \
+    VX = vb[j_ * 16 + su];                                                     \
   }
-  for (int64_t j0 = start; j0 < kend; j0 += 32) {
-    lds_barrier();                                     // the previous tile is consumed
-    ks[skey * 16 + (su ^ (skey & 15))] = kx0;
-    ks[skey * 16 + ((su + 1) ^ (skey & 15))] = kx1;
-    {
-      bf16_t* col = vt + 8 * su * BA_VT + skey;
-      col[0 * BA_VT] = (bf16_t)(vx0.x & 0xFFFF); col[1 * BA_VT] = (bf16_t)(vx0.x >> 16);
-      col[2 * BA_VT] = (bf16_t)(vx0.y & 0xFFFF); col[3 * BA_VT] = (bf16_t)(vx0.y >> 16);
-      col[4 * BA_VT] = (bf16_t)(vx0.z & 0xFFFF); col[5 * BA_VT] = (bf16_t)(vx0.z >> 16);
-      col[6 * BA_VT] = (bf16_t)(vx0.w & 0xFFFF); col[7 * BA_VT] = (bf16_t)(vx0.w >> 16);
-      col += 8 * BA_VT;
-      col[0 * BA_VT] = (bf16_t)(vx1.x & 0xFFFF); col[1 * BA_VT] = (bf16_t)(vx1.x >> 16);
-      col[2 * BA_VT] = (bf16_t)(vx1.y & 0xFFFF); col[3 * BA_VT] = (bf16_t)(vx1.y >> 16);
-      col[4 * BA_VT] = (bf16_t)(vx1.z & 0xFFFF); col[5 * BA_VT] = (bf16_t)(vx1.z >> 16);
-      col[6 * BA_VT] = (bf16_t)(vx1.w & 0xFFFF); col[7 * BA_VT] = (bf16_t)(vx1.w >> 16);
-    }
-    lds_barrier();                                     // the tile is staged
-    {                                                  // next tile (clamped: always a load)
-      const int64_t jn = j0 + 32 + skey;
-      const int64_t j = jn < cap ? jn : cap - 1;
-      kx0 = kb[j * 16 + su]; kx1 = kb[j * 16 + su + 1];
-      vx0 = vb[j * 16 + su]; vx1 = vb[j * 16 + su + 1];
-    }
+  auto stage = [&](const uint4& kx, const uint4& vx) {
+    ks[skey * 16 + (su ^ (skey & 15))] = kx;
+    bf16_t* col = vt + 8 * su * BA_VT + skey;
+    col[0 * BA_VT] = (bf16_t)(vx.x & 0xFFFF); col[1 * BA_VT] = (bf16_t)(vx.x >> 16);
+    col[2 * BA_VT] = (bf16_t)(vx.y & 0xFFFF); col[3 * BA_VT] = (bf16_t)(vx.y >> 16);
+    col[4 * BA_VT] = (bf16_t)(vx.z & 0xFFFF); col[5 * BA_VT] = (bf16_t)(vx.z >> 16);
+    col[6 * BA_VT] = (bf16_t)(vx.w & 0xFFFF); col[7 * BA_VT] = (bf16_t)(vx.w >> 16);
+  };
+  auto contract = [&](int64_t j0) {
     // S' = K . Q^T for both key halves and both row tiles
     f32x4_t sc[2][2];
 #pragma unroll
@@ -257,21 +248,34 @@ __global__ __launch_bounds__(256) void block_attn_mfma_kernel(
     // online softmax of both row tiles; P packed in the key order {4q4..+3, 16+4q4..+3}
     uint4 pf[2];
     float alpha[2];
+    // a tile of cached keys only (below base and kend) is visible to every row: no per-score
+    // test (the common case: all of the context but the block's own split)
+    const bool whole = j0 + 32 <= base && j0 + 32 <= kend;   // uniform over the workgroup
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       float sv[8];
+      if (whole) {
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2)
+        for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t j = j0 + 16 * h2 + 4 * q4 + r;
-          bool vis = j < kend;
-          if (j >= base) {
-            const int64_t jb = j - base;
-            vis = vis && (anc ? jb < 64 && ((mask[rt] >> (jb & 63)) & 1ull) != 0 : jb <= tok[rt]);
+          for (int r = 0; r < 4; ++r) sv[4 * h2 + r] = sc[rt][h2][r] * scale;
+      } else {
+        // key j = j0 + 16 h2 + 4 q4 + r, as offsets from the tile start and from base
+        const int jrel0 = (int)(j0 - base);                   // may be negative
+        const int lim = (int)(kend - j0);                     // keys of the tile below kend
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int o = 16 * h2 + 4 * q4 + r;
+            const int jb = jrel0 + o;                         // block index (< 0: cached key)
+            bool vis = o < lim;
+            if (jb >= 0)
+              vis = vis && (anc ? jb < 64 && ((mask[rt] >> (jb & 63)) & 1ull) != 0
+                                : (int64_t)jb <= tok[rt]);
+            sv[4 * h2 + r] = vis ? sc[rt][h2][r] * scale : NEG_INF;
           }
-          sv[4 * h2 + r] = vis ? sc[rt][h2][r] * scale : NEG_INF;
-        }
+      }
       float mx = sv[0];
 #pragma unroll
       for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
@@ -286,6 +290,14 @@ __global__ __launch_bounds__(256) void block_attn_mfma_kernel(
       lsum[rt] = lsum[rt] * alpha[rt] + ps;
       pf[rt] = make_uint4(pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7]));
     }
+    // rescale O only if some row's running max moved (alpha == 1 exactly otherwise, and
+    // x * 1 == x: skipping it changes no bit); wave-uniform
+    if (__ballot(alpha[0] != 1.f || alpha[1] != 1.f) != 0) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) o[rt][dt] *= alpha[rt];
+    }
     // O^T += V^T . P^T: V^T fragment of dims 16 dt + c, keys 4q4..+3 and 16+4q4..+3
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
@@ -294,14 +306,50 @@ __global__ __launch_bounds__(256) void block_attn_mfma_kernel(
       const uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * q4);
       const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        o[rt][dt] *= alpha[rt];
+      for (int rt = 0; rt < 2; ++rt)
         o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
             __builtin_bit_cast(bf16x8_t, vf), __builtin_bit_cast(bf16x8_t, pf[rt]), o[rt][dt], 0,
             0, 0);
-      }
     }
+  };
+  // Tile `it` is staged from ring slot it % 3 and the slot is then refilled with tile it + 3.
+  // The loop body is three tiles with no exit between them (an exit there lets the compiler
+  // sink a refill behind the contraction it should overlap); the last 0..2 tiles follow it.
+  uint4 k0, v0, k1, v1, k2, v2;
+  BA_LD(0, k0, v0);
+  BA_LD(1, k1, v1);
+  BA_LD(2, k2, v2);
+  int it = 0;
+  for (; it + 2 < ntiles; it += 3) {
+    lds_barrier();                                     // the previous tile is consumed
+    stage(k0, v0);
+    lds_barrier();                                     // the tile is staged
+    BA_LD(it + 3, k0, v0);
+    contract(start + 32 * (int64_t)it);
+    lds_barrier();
+    stage(k1, v1);
+    lds_barrier();
+    BA_LD(it + 4, k1, v1);
+    contract(start + 32 * (int64_t)(it + 1));
+    lds_barrier();
+    stage(k2, v2);
+    lds_barrier();
+    BA_LD(it + 5, k2, v2);
+    contract(start + 32 * (int64_t)(it + 2));
   }
+  if (it < ntiles) {
+    lds_barrier();
+    stage(k0, v0);
+    lds_barrier();
+    contract(start + 32 * (int64_t)it);
+  }
+  if (it + 1 < ntiles) {
+    lds_barrier();
+    stage(k1, v1);
+    lds_barrier();
+    contract(start + 32 * (int64_t)(it + 1));
+  }
+#undef BA_LD
   // per-row totals: the four q lanes of a row hold disjoint key subsets of l
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
@@ -309,7 +357,7 @@ __global__ __launch_bounds__(256) void block_attn_mfma_kernel(
     l += lane_xor16(l);
     l += lane_xor32(l);
     if (tok[rt] >= T) continue;
-    const int64_t idx = ((b * T + tok[rt]) * Hq + kvh * GRP + wave) * splits + split;
+    const int64_t idx = ((b * T + tok[rt]) * Hq + kvh * GRP + head) * splits + split;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
       *reinterpret_cast<f32x4_t*>(ws_acc + idx * 128 + 16 * dt + 4 * q4) = o[rt][dt];
@@ -325,7 +373,7 @@ void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_c
                        bf16_t* out, hipStream_t s) {
   if (B * T <= 0) return;
   const int64_t QB = (T + BA_TQ - 1) / BA_TQ;
-  block_attn_mfma_kernel<<<dim3((unsigned)splits, (unsigned)Hkv, (unsigned)(B * QB)), dim3(256), 0,
+  block_attn_mfma_kernel<<<dim3((unsigned)splits, (unsigned)Hkv, (unsigned)(B * QB)), dim3(512), 0,
                            s>>>(q, k_cache, v_cache, base, anc, T, Hq, Hkv, cap,
                                 1.0f / sqrtf(128.0f), ws_acc, ws_ml);
   attn_merge_kernel<<<dim3((unsigned)(B * T * Hq)), dim3(64), 0, s>>>(ws_acc, ws_ml, (int)splits,
