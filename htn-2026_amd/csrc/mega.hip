@@ -123,6 +123,17 @@ __device__ __forceinline__ void ll_fetch_lds(const uint64_t* src, int n, uint32_
     const int idx = threadIdx.x + j * MG_NT;
     v[j] = idx < n ? ll_raw(src + idx) : 0;
   }
+  // A word still stale here was most likely written while the loads were in flight, and so
+  // were the thread's other stale words: once the first one has arrived, re-issue all of them
+  // together (one round trip) instead of polling them one after the other.
+  if (WPT > 1 && threadIdx.x < n && !ll_ready(v[0], tag)) {
+    v[0] = ll_spin(src + threadIdx.x, tag, err);
+#pragma unroll
+    for (int j = 1; j < WPT; ++j) {
+      const int idx = threadIdx.x + j * MG_NT;
+      if (idx < n && !ll_ready(v[j], tag)) v[j] = ll_raw(src + idx);
+    }
+  }
 #pragma unroll
   for (int j = 0; j < WPT; ++j) {
     const int idx = threadIdx.x + j * MG_NT;
