@@ -1,6 +1,7 @@
 """Decode benchmark on one MI355X: Qwen3-4B-shaped bf16 greedy decode through the HIP engine.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-b32] [--no-tree] [--no-cpu]
+                    [--no-layer]
 
 Workloads:
   value  config 3 -- 36 layers, B=1, prompt 512, up to 256 new tokens: decode tok/s over K timed
@@ -10,6 +11,11 @@ Workloads:
   tree   config 5 -- tree verification, B=4, context 8192, 64-node random trees: the verify
          forward timed with HIP events (bytes/s and MFMA TFLOP/s), plus an end-to-end
          generate_tree (tokens per pass, wall-clock tok/s).
+  layer_kernels  config 2 -- embedding gather, residual-add + RMSNorm, QK-norm + RoPE (+ K/V
+         write), SwiGLU at B in {1, 8, 64}: us per launch (1000 launches in one hipGraph) and
+         algorithmic GB/s.
+  step_ms  per-step spread (median, p90, min, max) of the same K steps replayed again with an
+         event after each step (the headline timing has no events between steps).
 Weights are seeded random-init N(0, 0.02) generated on the device; prompt ids uniform.
 
 Roofline: at B=1 the step is ONE kernel (mega_step_kernel, the persistent decode step), so
@@ -86,10 +92,27 @@ def decode_run(eng, B, S, N, warmup, steps, seed):
     wall = time.perf_counter() - w0
     sh.decode.check()                                   # persistent step: no expired wait
     ms = e0.elapsed_time(e1) / K
+    # per-step spread: the same K steps again (pos rewound to the same context range), an
+    # event after every replay; kept out of the headline timing above
+    with torch.cuda.stream(st):
+        sh.kv.pos.fill_(S + warmup)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    with torch.cuda.stream(st):
+        ev[0].record(st)
+        for i in range(K):
+            sh.decode.replay()
+            ev[i + 1].record(st)
+    torch.cuda.synchronize()
+    sh.decode.check()
+    per = np.sort(np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(K)]))
+    spread = {"median": round(float(np.median(per)), 5),
+              "p90": round(float(per[min(K - 1, int(0.9 * K))]), 5),
+              "min": round(float(per[0]), 5), "max": round(float(per[-1]), 5)}
     ctx_mean = S + warmup + (K - 1) / 2.0 + 1           # keys read per step, averaged
     kv_bytes = B * ctx_mean * eng.model.kv_bytes_per_token
     step_bytes = eng.model.weight_bytes + kv_bytes
     return sh, {"B": B, "S": S, "K": K, "ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / K,
+                "step_ms": spread,
                 "step": "qd_mega_step (persistent)" if sh.decode.mega else "qd_decode_step",
                 "mega": sh.decode.mega,
                 "tok_s": B * 1e3 / ms, "prefill_s": prefill_s, "bytes_per_step": step_bytes,
@@ -201,6 +224,81 @@ def time_gu_kernel(eng, sh, reps=20):
     return us, nbytes
 
 
+def layer_kernels(reps=1000):
+    """Config 2: the fused layer kernels on their own, B in {1, 8, 64}, synthetic bf16 N(0, 1)
+    activations, positions uniform on [0, 8192).  Each kernel is captured `reps` times into one
+    hipGraph (fixed inputs and outputs) and the graph replayed; us_per_launch = replay time /
+    reps, so it includes the per-node launch cost of a graph (~1.6 us), which at these sizes
+    (10 KB - 3.7 MB) is most of it.  Bytes are the algorithmic ones: gather 2 B 5120;
+    add+RMSNorm 4 B 5120 + 5120; QK-norm+RoPE (q, k, v read and written) 2 B 48 256 + 2 B 256
+    (cos/sin rows); SwiGLU 3 B 19456."""
+    import ctypes as C
+
+    import torch
+    from qdecode import _lib, ops
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(7)
+    bf = torch.bfloat16
+    H, I, V, Hq, Hkv, cap = 2560, 9728, 151936, 32, 8, 8192
+    table = torch.randn((V, H), generator=g, device=dev).to(bf)
+    w = torch.ones(H, dtype=bf, device=dev)
+    cos = torch.randn((cap, 128), generator=g, device=dev).to(bf)
+    sin = torch.randn((cap, 128), generator=g, device=dev).to(bf)
+    qn = torch.ones(128, dtype=bf, device=dev)
+    st = torch.cuda.Stream()
+    out = []
+    for B in (1, 8, 64):
+        ids = torch.randint(0, V, (B,), generator=g, device=dev)
+        emb = torch.empty((B, H), dtype=bf, device=dev)
+        x = torch.randn((B, H), generator=g, device=dev).to(bf)
+        r = torch.randn((B, H), generator=g, device=dev).to(bf)
+        ro, y = torch.empty_like(r), torch.empty_like(r)
+        qkv = torch.randn((B, (Hq + 2 * Hkv) * 128), generator=g, device=dev).to(bf)
+        pos = torch.randint(0, cap, (B,), generator=g, device=dev)
+        q_out = torch.empty((B, 1, Hq, 128), dtype=bf, device=dev)
+        kc = torch.zeros((B, Hkv, cap, 128), dtype=bf, device=dev)
+        vc = torch.zeros_like(kc)
+        gu = torch.randn((B, 2 * I), generator=g, device=dev).to(bf)
+        act = torch.empty((B, I), dtype=bf, device=dev)
+        cases = [
+            ("embed_gather", 2 * B * H * 2, lambda: ops.embed_gather(ids, table, out=emb)),
+            ("add_rmsnorm", 4 * B * H * 2 + H * 2,
+             lambda: ops.add_rmsnorm(r, w, 1e-6, x=x, res_out=ro, y=y)),
+            ("qk_norm_rope", 2 * B * 48 * 256 + 2 * B * 256,
+             lambda: ops.qk_norm_rope(qkv, qn, qn, cos, sin, pos, ops.POS_ROW, q_out, kc, vc,
+                                      B, 1, Hq, Hkv, 1e-6)),
+            ("swiglu", 3 * B * I * 2, lambda: ops.swiglu(gu, out=act)),
+        ]
+        for name, nbytes, fn in cases:
+            torch.cuda.synchronize()
+            with torch.cuda.stream(st):
+                fn()                                     # argument checks outside the capture
+                _lib.call("qd_graph_begin", st.cuda_stream)
+                try:
+                    for _ in range(reps):
+                        fn()
+                finally:
+                    ex = C.c_void_p()
+                    rc = _lib.LIB.qd_graph_end(st.cuda_stream, C.byref(ex))
+                if rc != 0:
+                    raise _lib.QDError("qd_graph_end", rc)
+                _lib.call("qd_graph_launch", ex, st.cuda_stream)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(st):
+                e0.record(st)
+                for _ in range(3):
+                    _lib.call("qd_graph_launch", ex, st.cuda_stream)
+                e1.record(st)
+            torch.cuda.synchronize()
+            _lib.LIB.qd_graph_destroy(ex)
+            us = e0.elapsed_time(e1) * 1e3 / (3 * reps)
+            out.append({"kernel": name, "B": B, "us_per_launch": round(us, 3), "bytes": nbytes,
+                        "achieved_gbs": round(nbytes / (us * 1e-6) / 1e9, 1)})
+        del kc, vc
+    return out
+
+
 def cpu_baseline(budget_s=15.0, prompt_len=32):
     """The CPU oracle (torch CPU, oneDNN bf16) on the same 36-layer architecture and
     generator: prefill a short prompt, then time greedy decode steps for ~budget_s."""
@@ -250,6 +348,7 @@ def main():
     ap.add_argument("--no-b32", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-tree", action="store_true")
+    ap.add_argument("--no-layer", action="store_true", help="skip the config-2 kernel microbench")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB: the reference "
@@ -284,6 +383,17 @@ def main():
     us, gu_bytes = time_gu_kernel(eng, sh)
     log(f"gate/up GEMV: {us:.2f} us/launch, {gu_bytes / (us * 1e-6) / 1e9:.0f} GB/s")
 
+    layer = None
+    if not a.no_layer:
+        eng.shape = None
+        sh = None
+        torch.cuda.empty_cache()
+        layer = layer_kernels()
+        for c in layer:
+            log(f"config 2 {c['kernel']:>13} B={c['B']:>2}: {c['us_per_launch']:.2f} us/launch, "
+                f"{c['achieved_gbs']:.0f} GB/s")
+        torch.cuda.empty_cache()
+
     b32 = None
     if not a.no_b32:
         eng.shape = None
@@ -295,7 +405,7 @@ def main():
         b32 = {"workload": "config 4: 36 layers, B=32, prompts 2048, N=128", "steps": r32["K"],
                "decode_step": r32["step"],
                "warmup": 10, "ms_per_step": round(r32["ms_per_step"], 5),
-               "value": round(r32["tok_s"], 2), "unit": "tok/s",
+               "value": round(r32["tok_s"], 2), "unit": "tok/s", "step_ms": r32["step_ms"],
                "step_roofline": {"bound": "hbm", "achieved": round(r32["achieved_gbs"], 1),
                                  "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                  "frac": round(r32["achieved_gbs"] / PEAK_HBM_GBS, 4),
@@ -353,9 +463,11 @@ def main():
                           "frac": round(r1["achieved_gbs"] / PEAK_HBM_GBS, 4),
                           "bytes_per_step": int(r1["bytes_per_step"])},
         "wall_ms_per_step": round(r1["wall_ms_per_step"], 5),
+        "step_ms": r1["step_ms"],
         "prefill_s": round(r1["prefill_s"], 3),
         "b32": b32,
         "tree": tree,
+        "layer_kernels": layer,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
