@@ -286,6 +286,207 @@ __global__ __launch_bounds__(512) void gemm_lds_kernel(
                               res_stride, pval, pidx, logits);
 }
 
+// ------------------------------------------------------------------ streaming kernel (M <= 64)
+// Weight-streaming MFMA GEMM for few activation rows (batched decode, small trees): the weights
+// are read once and are the whole cost, so the design is about keeping every CU's share of the
+// HBM stream going.  One workgroup per CU (grid = CU count; its LDS footprint keeps a second
+// one off the CU), each owning a contiguous run of output units for the whole of K -- weight
+// rows, or act rows (a gate row and its up row) for SwiGLU -- so every CU streams the same
+// number of bytes and no split-K partials exist.
+//  * Units are taken in passes of G 16-unit MFMA tiles; a step is one 512-wide K chunk of one
+//    pass: the pass's weight rows (zeros past the run: padding is never read from HBM) and the
+//    MT*16 activation rows (zeros past M) are staged in LDS, each row chunk one 1 KiB-contiguous
+//    load instruction, written at unit i ^ (row & 15) (fragment reads hit 16 bank groups).
+//  * NB steps are in flight in registers (a ring refilled as each step is staged); the ring
+//    runs across pass boundaries, so the stream does not drain between passes.
+//  * Output block (tile t, activation tile mt) belongs to one wave for the whole of K
+//    (mt = wave % MT): no cross-wave reduction; the epilogue runs after a pass's last chunk.
+// Accumulation is fp32 in k order within the chunk's 16 MFMAs; only the summation order
+// differs from the reference.
+// Used for the LM head (argmax epilogue, ~600 rows per workgroup).  For the projections
+// (10-76 rows per workgroup at 256 CUs) re-staging the activation rows with every chunk costs
+// more than the even split gains (measured at 32 rows: qkv 17.4 vs 13.7 us, gate/up 39.4 vs
+// 30.4 us), so they stay on gemm_lds_kernel.
+template <int MT, int EPI, int G>
+constexpr int stream_nb() {
+  constexpr int sr = (EPI == EPI_SWIGLU ? 2 : 1) * G * 16 + MT * 16;
+  constexpr int lpw = sr / 8;
+  return lpw <= 6 ? 4 : lpw <= 12 ? 3 : 2;
+}
+
+template <int MT, int EPI, int G, int NB>
+__global__ __launch_bounds__(512) void gemm_stream_kernel(
+    const bf16_t* __restrict__ X, int64_t x_stride, int M, const bf16_t* __restrict__ W, int N,
+    int K, bf16_t* out, int64_t out_stride, const bf16_t* res, int64_t res_stride, float* pval,
+    int32_t* pidx, float* logits) {
+  constexpr bool SW = EPI == EPI_SWIGLU, AM = EPI == EPI_ARGMAX;
+  constexpr int NWV = 8;
+  constexpr int TU = G * 16;                    // units per pass
+  constexpr int WR = SW ? 2 * TU : TU;          // staged weight rows (gate rows, then up rows)
+  constexpr int XR = MT * 16;                   // staged activation rows
+  constexpr int SR = WR + XR;
+  static_assert(SR % NWV == 0 && NWV % MT == 0, "rows per wave");
+  constexpr int LPW = SR / NWV;                 // row-chunk loads per wave per step
+  constexpr int NBLK = G * MT;                  // output blocks per pass
+  constexpr int BPW = (NBLK + NWV - 1) / NWV;   // blocks per wave
+  constexpr int LDS_U4 = SR * 64 > 5248 ? SR * 64 : 5248;   // >= 82 KiB: one workgroup per CU
+  __shared__ uint4 stage[LDS_U4];
+  __shared__ float am_v[AM ? NWV : 1][AM ? XR : 1];
+  __shared__ int32_t am_i[AM ? NWV : 1][AM ? XR : 1];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
+  const int mt = wave % MT;                     // this wave's activation tile
+  const int P = gridDim.x, wg = blockIdx.x;
+  const int64_t u0 = (int64_t)N * wg / P, u1 = (int64_t)N * (wg + 1) / P;
+  const int npass = (int)((u1 - u0 + TU - 1) / TU);
+  const int nchunks = K / 512;
+  const int S = npass * nchunks;                // steps (pass, chunk), chunk fastest
+  uint4 buf[NB][LPW];
+  // step s into ring slot b; a step past the end loads only activation rows (no HBM bytes)
+  auto load = [&](int b, int s) {
+    const int p = s / nchunks, kc = s - p * nchunks;
+    const int64_t t0 = u0 + (int64_t)p * TU;
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int rr = wave + NWV * j;
+      if (rr < WR) {
+        const int u = rr % TU;
+        const bool ok = s < S && t0 + u < u1;
+        const int64_t row = (ok ? t0 + u : 0) + (rr >= TU ? N : 0);
+        const uint4* src = reinterpret_cast<const uint4*>(W + row * K) + kc * 64 + lane;
+        buf[b][j] = ok ? ld_stream(src) : make_uint4(0, 0, 0, 0);
+      } else {
+        const int m = rr - WR;
+        const uint4 v = reinterpret_cast<const uint4*>(X + (int64_t)(m < M ? m : 0) * x_stride)[kc * 64 + lane];
+        buf[b][j] = m < M ? v : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  auto store = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int rr = wave + NWV * j;
+      stage[rr * 64 + (lane ^ (rr & 15))] = buf[b][j];
+    }
+  };
+  f32x4_t acc[BPW], acc2[SW ? BPW : 1];
+  auto zero = [&]() {
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+      acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if constexpr (SW) acc2[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  zero();
+  auto compute = [&]() {
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+      const int blk = wave + NWV * i;
+      if (blk < NBLK) {
+        const int t = blk / MT;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {          // k = 32 s + 8 q .. +7 of the chunk
+          const int u = (4 * s + q) ^ c;
+          const uint4 xf = stage[(WR + 16 * mt + c) * 64 + u];
+          const uint4 wf = stage[(16 * t + c) * 64 + u];
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xf), as_bf8(wf), acc[i], 0, 0, 0);
+          if constexpr (SW) {
+            const uint4 uf = stage[(TU + 16 * t + c) * 64 + u];
+            acc2[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xf), as_bf8(uf), acc2[i], 0, 0, 0);
+          }
+        }
+      }
+    }
+  };
+  // argmax state: lane (c, q) tracks rows m = 16 mt + 4 q + r over its columns
+  float bv[4];
+  int32_t bi[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) { bv[r] = -INFINITY; bi[r] = 0x7FFFFFFF; }
+  // D of a block: lane (c, q) holds rows m = 16 mt + 4 q + r (r < 4) of unit column 16 t + c
+  auto epilogue = [&](int p) {
+    const int64_t t0 = u0 + (int64_t)p * TU;
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+      const int blk = wave + NWV * i;
+      if (blk < NBLK) {
+        const int64_t n = t0 + 16 * (blk / MT) + c;
+        if (n < u1) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = 16 * mt + 4 * q + r;
+            if (m >= M) continue;
+            const float v = acc[i][r];
+            if constexpr (AM) {
+              if (logits) logits[m * (int64_t)N + n] = v;
+              const float vb = rbf(v);            // the reference's logits are bf16
+              if (vb > bv[r]) { bv[r] = vb; bi[r] = (int32_t)n; }   // n ascends per lane
+            } else {
+              float y;
+              if constexpr (EPI == EPI_RES) {
+                y = bf2f(res[m * res_stride + n]) + rbf(v);
+              } else if constexpr (SW) {
+                y = rbf(silu_f(rbf(v))) * rbf(acc2[i][r]);
+              } else {
+                y = v;
+              }
+              out[m * out_stride + n] = (bf16_t)f2bf(y);
+            }
+          }
+        }
+      }
+    }
+    zero();
+  };
+#pragma unroll
+  for (int b = 0; b < NB; ++b) load(b, b);
+  for (int s0 = 0; s0 < S; s0 += NB) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int s = s0 + b;
+      if (s < S) {
+        lds_barrier();                           // the previous step's fragments are read
+        store(b);
+        load(b, s + NB);
+        lds_barrier();                           // this step is staged
+        compute();
+        const int p = s / nchunks;
+        if (s - p * nchunks == nchunks - 1) epilogue(p);
+      }
+    }
+  }
+  if constexpr (AM) {
+    // best per row over the 16 columns of a lane group, then over the waves of this tile
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) {
+        const float v2 = __shfl_xor(bv[r], off, 64);
+        const int32_t i2 = __shfl_xor(bi[r], off, 64);
+        if (v2 > bv[r] || (v2 == bv[r] && i2 < bi[r])) { bv[r] = v2; bi[r] = i2; }
+      }
+    }
+    for (int e = lane; e < XR; e += 64) { am_v[wave][e] = -INFINITY; am_i[wave][e] = 0x7FFFFFFF; }
+    __syncthreads();
+    if (c == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) { am_v[wave][16 * mt + 4 * q + r] = bv[r]; am_i[wave][16 * mt + 4 * q + r] = bi[r]; }
+    }
+    __syncthreads();
+    for (int m = threadIdx.x; m < M && m < XR; m += NWV * 64) {
+      float v = am_v[0][m];
+      int32_t ix = am_i[0][m];
+      for (int w2 = 1; w2 < NWV; ++w2) {
+        const float v2 = am_v[w2][m];
+        const int32_t i2 = am_i[w2][m];
+        if (v2 > v || (v2 == v && i2 < ix)) { v = v2; ix = i2; }
+      }
+      pval[m * (int64_t)P + wg] = v;
+      pidx[m * (int64_t)P + wg] = ix;
+    }
+  }
+}
+
 int64_t gemm_argmax_parts(int64_t N) { return (N + 15) / 16; }
 
 // Waves per workgroup and groups per pass from the number of 128-wide K groups: K <= 2560 -> 4
@@ -329,6 +530,43 @@ static void gemm_lds_go(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w,
                                                           os, res, rs, pval, pidx, logits);
 }
 
+// one workgroup per CU
+static int stream_grid() {
+  static int grid = -1;
+  if (grid < 0) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      cus = 0;
+    }
+    grid = cus;
+  }
+  return grid;
+}
+
+template <int MT, int EPI, int G>
+static void stream_go(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
+                      int64_t K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs,
+                      float* pval, int32_t* pidx, float* logits, int P, hipStream_t s) {
+  constexpr int NB = stream_nb<MT, EPI, G>();
+  gemm_stream_kernel<MT, EPI, G, NB><<<dim3((unsigned)P), dim3(512), 0, s>>>(
+      x, xs, (int)M, w, (int)N, (int)K, out, os, res, rs, pval, pidx, logits);
+}
+
+// Passes of G tiles from the units per workgroup: o / down (10 units at 256 CUs) one tile,
+// qkv (24) two, gate/up (38 act rows) three gate + three up tiles (two at 64 rows, where the
+// activation tiles take the LDS), the LM head (594) four per pass.
+// The LM head: four 16-row tiles per pass (~600 rows per workgroup at 256 CUs).
+template <int MT, int EPI>
+static int64_t stream_mt(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
+                         int64_t K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs,
+                         float* pval, int32_t* pidx, float* logits, int P, hipStream_t s) {
+  static_assert(EPI == EPI_ARGMAX, "the streaming kernel serves the LM head");
+  stream_go<MT, EPI, 4>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, P, s);
+  return P;
+}
+
 template <int EPI>
 static int64_t gemm_mt(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
                        int64_t K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs,
@@ -337,6 +575,19 @@ static int64_t gemm_mt(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, 
   if (M >= GEMM_TILE_MIN_M && gemm_tile_ok(M, N, K, EPI, x, xs, w, out, os, res, rs))
     return launch_gemm_tile(x, xs, M, w, N, K, out, os, res, rs, EPI, pval, pidx, logits, part,
                             part_floats, s);
+  const int P = stream_grid();
+  const bool aligned = xs % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(w) % 16 == 0;
+  // the LM head: ~600 rows per workgroup, so the per-chunk activation re-reads are small next
+  // to the weight rows (measured 223 vs 238 us at 32 rows); the projections (10-76 rows per
+  // workgroup) stay on the LDS-staged kernel, where the activation re-reads dominated
+  if constexpr (EPI == EPI_ARGMAX) {
+    if (M <= 64 && K % 512 == 0 && aligned && P >= 1) {
+      if (M <= 16) return stream_mt<1, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, P, s);
+      if (M <= 32) return stream_mt<2, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, P, s);
+      return stream_mt<4, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, P, s);
+    }
+  }
   if (M <= 64 && K % 512 == 0) {
     if (M <= 16) gemm_lds_go<1, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
     else gemm_lds_go<2, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
