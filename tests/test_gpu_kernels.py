@@ -201,7 +201,9 @@ def test_linear_epilogues(ops, name, B):
 
 
 # ------------------------------------------------------------------ LM head + argmax
-@pytest.mark.parametrize("B", [1, 2, 8, 72])
+# 1-2 rows: the vector kernel; 3-64: the weight-streaming MFMA kernel (16 / 32 / 64-row
+# activation tiles); 72: the tiled kernel
+@pytest.mark.parametrize("B", [1, 2, 8, 24, 40, 72])
 def test_lm_head_argmax(ops, B):
     say(f"lm_head_argmax B={B}")
     g = torch.Generator().manual_seed(400 + B)
@@ -230,7 +232,7 @@ def test_lm_head_argmax(ops, B):
     assert int(pos.item()) == 1                                  # position advanced once
 
 
-@pytest.mark.parametrize("B", [1, 8, 72])
+@pytest.mark.parametrize("B", [1, 8, 40, 72])
 def test_lm_head_ties_pick_lowest_index(ops, B):
     say(f"lm_head ties B={B}")
     V, K = 151936, 2560
