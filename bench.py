@@ -41,14 +41,14 @@ sys.path.insert(0, os.path.join(ROOT, "htn-2026_amd"))
 
 PEAK_HBM_GBS = 8000.0
 # HBM bytes per gate/up launch at B=1, from two rocprofv3 --pmc passes over this script
-# (`--calib-copy-mib 512`): FETCH_SIZE 48,701.0 KiB x 1.99987 + WRITE_SIZE 38.0 KiB x 1.0, the
+# (`--calib-copy-mib 512`): FETCH_SIZE 48,703.0 KiB x 1.99986 + WRITE_SIZE 38.0 KiB x 1.0, the
 # factors being what the same counters read for a 512 MiB device copy.  Summary and commands:
 # profiles/gemv_gate_up_b1_traffic.md.
-GU_TRAFFIC_B1 = 99_771_853
-# HBM bytes per persistent-step launch at B=1 (config 3), same method (FETCH_SIZE 4,025,561.9
-# KiB x 1.99987 + WRITE_SIZE 47,564.1 KiB), mean over the profiled steps at positions 512..520;
+GU_TRAFFIC_B1 = 99_775_769
+# HBM bytes per persistent-step launch at B=1 (config 3), same method (FETCH_SIZE 4,028,087.2
+# KiB x 1.99986 + WRITE_SIZE 48,588.1 KiB), mean over the profiled steps at positions 512..520;
 # summary and commands: profiles/mega_step_b1_traffic.md.
-MEGA_TRAFFIC_B1 = 8_292_506_053
+MEGA_TRAFFIC_B1 = 8_298_707_242
 METRIC = "decode tok/s (Qwen3-4B bf16, B=1 & B=32) + achieved HBM GB/s vs peak"
 
 
