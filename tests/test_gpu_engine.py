@@ -134,9 +134,11 @@ def ref2():
     return R.Qwen3Ref.from_synth(1, 2)
 
 
-@pytest.mark.parametrize("B,S,N", [(2, 33, 8), (5, 40, 6), (32, 64, 6)])
+@pytest.mark.parametrize("B,S,N", [(2, 33, 8), (5, 40, 6), (32, 64, 6), (64, 24, 4), (80, 16, 4)])
 def test_batched_decode_paths(eng2, ref2, B, S, N):
-    say(f"batched decode B={B} S={S} N={N} (vector path B<=2, MFMA path B>=3)")
+    """Vector path B <= 2; LDS-staged MFMA GEMMs + streaming LM head 3..64 rows (16-, 32- and
+    two 32-row activation tiles); the tiled GEMMs past 64 rows."""
+    say(f"batched decode B={B} S={S} N={N}")
     prompt = synth.prompt_ids(20 + B, B, S)
     toks = np.array(list(eng2.generate(prompt.tolist(), N))).T
     tl = ref2.teacher_logits(prompt, toks)
