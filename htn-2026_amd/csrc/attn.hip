@@ -150,16 +150,27 @@ constexpr int64_t BLOCK_CHUNK = 512;
 //    4q..4q+3 and 16+4q..16+4q+3 of the tile;
 //  * online softmax per query row in fp32 (the row max / sum across the four q lanes through
 //    permlane swaps), P rounded to bf16;
-//  * O^T += V^T . P^T: A = V^T rows (LDS, stored transposed with a padded stride), B = the lane's
-//    8 probabilities, taken in that same key order (a permutation of the contraction index shared
-//    by both operands), so O^T's lane (c, q) holds dims 16 dt + 4q..+3 of row c and the per-row
-//    rescale needs no cross-lane traffic;
+//  * O^T += V^T . P^T: A = V^T fragments, B = the lane's 8 probabilities, taken in that same key
+//    order (a permutation of the contraction index shared by both operands), so O^T's lane (c, q)
+//    holds dims 16 dt + 4q..+3 of row c and the per-row rescale needs no cross-lane traffic.  V is
+//    staged key-major like K (one 16-byte store per thread) and read transposed with gfx950's
+//    ds_read_b64_tr_b16: within a 16-lane group, lane j = 4a + b receives element b of the
+//    8-byte pieces that lanes a, a + 4, a + 8, a + 12 address, so lane i addressing dims
+//    16 dt + 4 (i % 4) .. + 3 of key 4q + i / 4 makes lane c receive V[4q + r][16 dt + c],
+//    r = 0..3 (measured on MI355X with an in-bounds layout probe);
 //  * staging: thread i moves K and V unit i % 16 of key i / 16 of a tile; the next three tiles'
 //    loads are in flight (a register ring) while a tile is staged and contracted.
 // Writes (m, l, acc) partials per (query row, head, split) -- ws_acc[idx * 128 + d], ws_ml[idx * 2],
 // idx = ((b*T + t)*Hq + h)*splits + split -- which attn_merge_kernel merges.
 constexpr int BA_TQ = 64;
-constexpr int BA_VT = 36;  // V^T row stride (bf16): 72 bytes, 16 rows hit 32 distinct banks
+
+typedef short ba_v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) ba_v4i16_t ba_lds_v4i16_t;
+// four bf16 of the transposed 16-lane read at p (LDS), as two packed 32-bit words
+__device__ __forceinline__ uint2 lds_read_tr16(const void* p) {
+  const ba_v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((ba_lds_v4i16_t*)p);
+  return __builtin_bit_cast(uint2, r);
+}
 
 __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
@@ -169,7 +180,7 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
   typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
   typedef __attribute__((ext_vector_type(4))) float f32x4_t;
   __shared__ uint4 ks[32 * 16];
-  __shared__ bf16_t vt[128 * BA_VT];
+  __shared__ uint4 vs[32 * 16];
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int splits = gridDim.x;
   const int64_t QB = (T + BA_TQ - 1) / BA_TQ;
@@ -219,11 +230,14 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
   }
   auto stage = [&](const uint4& kx, const uint4& vx) {
     ks[skey * 16 + (su ^ (skey & 15))] = kx;
-    bf16_t* col = vt + 8 * su * BA_VT + skey;
-    col[0 * BA_VT] = (bf16_t)(vx.x & 0xFFFF); col[1 * BA_VT] = (bf16_t)(vx.x >> 16);
-    col[2 * BA_VT] = (bf16_t)(vx.y & 0xFFFF); col[3 * BA_VT] = (bf16_t)(vx.y >> 16);
-    col[4 * BA_VT] = (bf16_t)(vx.z & 0xFFFF); col[5 * BA_VT] = (bf16_t)(vx.z >> 16);
-    col[6 * BA_VT] = (bf16_t)(vx.w & 0xFFFF); col[7 * BA_VT] = (bf16_t)(vx.w >> 16);
+    vs[skey * 16 + (su ^ (skey & 15))] = vx;
+  };
+  // this lane's transposed-read address for V dims 16 dt + 4 (c % 4) .. + 3 of key 16 h2 + 4 q4 +
+  // c / 4: 16-byte unit 2 dt + (c / 2) % 2, half c % 2
+  auto vt_addr = [&](int dt, int h2) -> const void* {
+    const int key = 16 * h2 + 4 * q4 + (c >> 2);
+    const int u = 2 * dt + ((c >> 1) & 1);
+    return reinterpret_cast<const char*>(&vs[key * 16 + (u ^ (key & 15))]) + 8 * (c & 1);
   };
   auto contract = [&](int64_t j0) {
     // S' = K . Q^T for both key halves and both row tiles
@@ -301,9 +315,8 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
     // O^T += V^T . P^T: V^T fragment of dims 16 dt + c, keys 4q4..+3 and 16+4q4..+3
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      const bf16_t* row = vt + (16 * dt + c) * BA_VT;
-      const uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * q4);
-      const uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * q4);
+      const uint2 lo = lds_read_tr16(vt_addr(dt, 0));
+      const uint2 hi = lds_read_tr16(vt_addr(dt, 1));
       const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
