@@ -82,6 +82,8 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
   return t;
 }
 
+constexpr int AR_MAXC = 4;   // 16-byte chunks per thread held in registers (hidden <= 8192)
+
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
     const bf16_t* __restrict__ x, const bf16_t* res, const bf16_t* __restrict__ w,
     bf16_t* res_out, bf16_t* __restrict__ y, int64_t hidden, int64_t in_stride,
@@ -92,39 +94,55 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
   const uint4* xr = x ? reinterpret_cast<const uint4*>(x + row * in_stride) : nullptr;
   const uint4* rr = reinterpret_cast<const uint4*>(res + row * in_stride);
   uint4* ro = res_out ? reinterpret_cast<uint4*>(res_out + row * in_stride) : nullptr;
-  float ss = 0.f;
-  for (int64_t c = threadIdx.x; c < nch; c += 256) {
-    uint4 r = rr[c];
-    if (xr) {
-      uint4 a = xr[c];
-      r.x = pack2(bflo(a.x) + bflo(r.x), bfhi(a.x) + bfhi(r.x));
-      r.y = pack2(bflo(a.y) + bflo(r.y), bfhi(a.y) + bfhi(r.y));
-      r.z = pack2(bflo(a.z) + bflo(r.z), bfhi(a.z) + bfhi(r.z));
-      r.w = pack2(bflo(a.w) + bflo(r.w), bfhi(a.w) + bfhi(r.w));
-    }
-    ss += bflo(r.x) * bflo(r.x) + bfhi(r.x) * bfhi(r.x) + bflo(r.y) * bflo(r.y) +
-          bfhi(r.y) * bfhi(r.y) + bflo(r.z) * bflo(r.z) + bfhi(r.z) * bfhi(r.z) +
-          bflo(r.w) * bflo(r.w) + bfhi(r.w) * bfhi(r.w);
-  }
-  const float rstd = rstd_of(block_sum256(ss, red), (int)hidden, eps);
   const uint4* wr = reinterpret_cast<const uint4*>(w);
   uint4* yr = reinterpret_cast<uint4*>(y + row * y_stride);
-  for (int64_t c = threadIdx.x; c < nch; c += 256) {
-    uint4 r = rr[c];
+  auto add = [&](uint4 r, int64_t c) {
     if (xr) {
-      uint4 a = xr[c];
+      const uint4 a = xr[c];
       r.x = pack2(bflo(a.x) + bflo(r.x), bfhi(a.x) + bfhi(r.x));
       r.y = pack2(bflo(a.y) + bflo(r.y), bfhi(a.y) + bfhi(r.y));
       r.z = pack2(bflo(a.z) + bflo(r.z), bfhi(a.z) + bfhi(r.z));
       r.w = pack2(bflo(a.w) + bflo(r.w), bfhi(a.w) + bfhi(r.w));
     }
-    const uint4 g = wr[c];
+    return r;
+  };
+  auto norm_out = [&](const uint4 r, const uint4 g, float rstd) {
     uint4 o;
     o.x = pack2(norm_elem(bflo(r.x), rstd, bflo(g.x)), norm_elem(bfhi(r.x), rstd, bfhi(g.x)));
     o.y = pack2(norm_elem(bflo(r.y), rstd, bflo(g.y)), norm_elem(bfhi(r.y), rstd, bfhi(g.y)));
     o.z = pack2(norm_elem(bflo(r.z), rstd, bflo(g.z)), norm_elem(bfhi(r.z), rstd, bfhi(g.z)));
     o.w = pack2(norm_elem(bflo(r.w), rstd, bflo(g.w)), norm_elem(bfhi(r.w), rstd, bfhi(g.w)));
-    yr[c] = o;
+    return o;
+  };
+  float ss = 0.f;
+  if (nch <= 256 * AR_MAXC) {
+    // the row (and the norm weights) stay in registers across the reduction: one pass of loads
+    uint4 rv[AR_MAXC], gv[AR_MAXC];
+#pragma unroll
+    for (int j = 0; j < AR_MAXC; ++j) {
+      const int64_t c = threadIdx.x + 256 * j;
+      if (c < nch) {
+        rv[j] = add(rr[c], c);
+        gv[j] = wr[c];
+        ss += sumsq8(rv[j]);
+      }
+    }
+    const float rstd = rstd_of(block_sum256(ss, red), (int)hidden, eps);
+#pragma unroll
+    for (int j = 0; j < AR_MAXC; ++j) {
+      const int64_t c = threadIdx.x + 256 * j;
+      if (c < nch) {
+        yr[c] = norm_out(rv[j], gv[j], rstd);
+        if (ro && xr) ro[c] = rv[j];
+      }
+    }
+    return;
+  }
+  for (int64_t c = threadIdx.x; c < nch; c += 256) ss += sumsq8(add(rr[c], c));
+  const float rstd = rstd_of(block_sum256(ss, red), (int)hidden, eps);
+  for (int64_t c = threadIdx.x; c < nch; c += 256) {
+    const uint4 r = add(rr[c], c);
+    yr[c] = norm_out(r, wr[c], rstd);
     // each thread writes back exactly the chunks it read, after its last read of them
     if (ro && xr) ro[c] = r;
   }
