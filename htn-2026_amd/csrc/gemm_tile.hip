@@ -275,8 +275,19 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
   const int64_t n4 = N / 4;
   if (g >= M * n4) return;
   const int64_t m = g / n4, n = 4 * (g % n4);
+  // partials summed in split order, loaded eight at a time before any of them is added
+  constexpr int RB = 8;
   f32x4_t a = *reinterpret_cast<const f32x4_t*>(part + m * N + n);
-  for (int z = 1; z < splits; ++z) a += *reinterpret_cast<const f32x4_t*>(part + ((int64_t)z * M + m) * N + n);
+  for (int z0 = 1; z0 < splits; z0 += RB) {
+    f32x4_t v[RB];
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+      v[i] = z0 + i < splits ? *reinterpret_cast<const f32x4_t*>(part + ((int64_t)(z0 + i) * M + m) * N + n)
+                             : f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+      if (z0 + i < splits) a += v[i];
+  }
   float y[4];
   if constexpr (EPI == EPI_RES) {
     const uint2 rv = *reinterpret_cast<const uint2*>(res + m * res_stride + n);
