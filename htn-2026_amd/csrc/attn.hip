@@ -141,7 +141,7 @@ constexpr int64_t BLOCK_CHUNK = 512;
 // Block attention for T query tokens per sequence (tree verification with ancestor masks, causal
 // prefill chunks): query token t of sequence b sees every cached key < base[b] and block key
 // base[b] + j iff bit j of anc[b*T + t] (tree.py:72-195, engine.py:445-461) or j <= t (causal).
-// v_mfma_f32_16x16x32_bf16.  Workgroup = (key split of BLOCK_CHUNK keys, KV head, block of
+// v_mfma_f32_16x16x32_bf16.  Workgroup = (key split of `chunk` keys, KV head, block of
 // BA_TQ = 64 query tokens of one sequence), 8 waves: wave w handles query head kvh*4 + (w & 3)
 // for the block's tokens 32 (w >> 2) .. + 31 (two 16-row tiles), so every staged K/V tile
 // serves 64 tokens x 4 heads.  Keys go in tiles of 32:
@@ -175,8 +175,8 @@ __device__ __forceinline__ uint2 lds_read_tr16(const void* p) {
 __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
     const bf16_t* __restrict__ v_cache, const int64_t* __restrict__ base_ptr,
-    const uint64_t* __restrict__ anc, int64_t T, int Hq, int Hkv, int64_t cap, float scale,
-    float* ws_acc, float* ws_ml) {
+    const uint64_t* __restrict__ anc, int64_t T, int Hq, int Hkv, int64_t cap, int64_t chunk,
+    float scale, float* ws_acc, float* ws_ml) {
   typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
   typedef __attribute__((ext_vector_type(4))) float f32x4_t;
   __shared__ uint4 ks[32 * 16];
@@ -204,8 +204,8 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
     for (int kk = 0; kk < 4; ++kk) qf[rt][kk] = qr[4 * kk + q4];
     mask[rt] = anc ? anc[b * T + tt] : 0;
   }
-  const int64_t start = (int64_t)split * BLOCK_CHUNK;
-  int64_t kend = start + BLOCK_CHUNK;
+  const int64_t start = (int64_t)split * chunk;
+  int64_t kend = start + chunk;
   if (kend > base + T) kend = base + T;
   if (!anc && kend > base + tb + BA_TQ) kend = base + tb + BA_TQ;   // causal: later keys unseen
   if (kend > cap) kend = cap;
@@ -378,7 +378,29 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
   }
 }
 
+// the most splits (BLOCK_CHUNK keys each) a launch may use: what the workspace is sized for
 int64_t block_attn_splits(int64_t cap) { return (cap + BLOCK_CHUNK - 1) / BLOCK_CHUNK; }
+
+// Key splits are only there to fill the chip when few query blocks exist (a tree verification:
+// B blocks per KV head).  Every extra split writes and re-reads a full set of fp32 partials for
+// every query row, and the kernel runs one 8-wave workgroup per CU (its registers), so the
+// launch uses as many splits as fit in ONE round of workgroups over the CUs (at least one), each
+// covering a whole number of 32-key tiles.  Measured on MI355X (config 5): 17 splits of 512
+// keys (544 workgroups, a 1/8-full third round) 10.44 ms per verify forward, 16 splits 9.66 ms,
+// 8 splits 9.08 ms; the 4 x 8192 prefill 0.69 -> 0.59 s with one split instead of 17.
+static int64_t block_attn_cus() {
+  static int64_t cus = -1;
+  if (cus < 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 256;
+    }
+    cus = n > 0 ? n : 256;
+  }
+  return cus;
+}
 
 void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
                        const int64_t* base, const uint64_t* anc, int64_t B, int64_t T, int Hq,
@@ -386,9 +408,16 @@ void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_c
                        bf16_t* out, hipStream_t s) {
   if (B * T <= 0) return;
   const int64_t QB = (T + BA_TQ - 1) / BA_TQ;
-  block_attn_mfma_kernel<<<dim3((unsigned)splits, (unsigned)Hkv, (unsigned)(B * QB)), dim3(512), 0,
-                           s>>>(q, k_cache, v_cache, base, anc, T, Hq, Hkv, cap,
+  const int64_t blocks = (int64_t)Hkv * B * QB;
+  int64_t use = block_attn_cus() / blocks;
+  if (use > splits) use = splits;
+  if (use < 1) use = 1;
+  int64_t chunk = (cap + use - 1) / use;
+  chunk = (chunk + 31) / 32 * 32;
+  use = (cap + chunk - 1) / chunk;                      // no empty trailing split
+  block_attn_mfma_kernel<<<dim3((unsigned)use, (unsigned)Hkv, (unsigned)(B * QB)), dim3(512), 0,
+                           s>>>(q, k_cache, v_cache, base, anc, T, Hq, Hkv, cap, chunk,
                                 1.0f / sqrtf(128.0f), ws_acc, ws_ml);
-  attn_merge_kernel<<<dim3((unsigned)(B * T * Hq)), dim3(64), 0, s>>>(ws_acc, ws_ml, (int)splits,
+  attn_merge_kernel<<<dim3((unsigned)(B * T * Hq)), dim3(64), 0, s>>>(ws_acc, ws_ml, (int)use,
                                                                       out);
 }
