@@ -205,8 +205,12 @@ __global__ __launch_bounds__(512) void gemm_lds_kernel(
   constexpr int R = WR + XR;
   static_assert(R % NWV == 0, "rows per wave");
   constexpr int LPW = R / NWV;                   // row-chunk loads per wave per chunk
-  __shared__ uint4 stage[R * 64];                // R rows x 64 units of 16 B (512 k)
-  __shared__ EpiLds<MT, EPI, NWV> esm;
+  // R rows x 64 units of 16 B (512 k); after the last chunk the same LDS holds the epilogue's
+  // cross-wave sums, so a workgroup needs only the staging bytes (two workgroups per CU with
+  // the SwiGLU pair's 64 rows)
+  constexpr int EPI_U4 = (int)((sizeof(EpiLds<MT, EPI, NWV>) + 15) / 16);
+  __shared__ uint4 stage[R * 64 > EPI_U4 ? R * 64 : EPI_U4];
+  EpiLds<MT, EPI, NWV>& esm = *reinterpret_cast<EpiLds<MT, EPI, NWV>*>(stage);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = lane & 15, q = lane >> 4;
   const int64_t m0 = (int64_t)blockIdx.x * XR;
@@ -282,6 +286,7 @@ __global__ __launch_bounds__(512) void gemm_lds_kernel(
       }
     }
   }
+  lds_barrier();                                 // every wave is done with the staged rows
   gemm_epilogue<MT, EPI, NWV>(esm, acc, SW ? acc2 : nullptr, m0, n0, M, N, out, out_stride, res,
                               res_stride, pval, pidx, logits);
 }
