@@ -318,13 +318,30 @@ bool gemm_tile_ok(int64_t M, int64_t N, int64_t K, int epi, const void* x, int64
   return M * (int64_t)(N / 16) < (1ll << 40) && (M + TM - 1) / TM * tile_nblocks(N, epi) < (1ll << 30);
 }
 
-// K splits: only the store / residual epilogues split; enough to put ~256 workgroups in flight,
-// keeping at least 4 stages per split
+static int64_t tile_cus() {
+  static int64_t cus = -1;
+  if (cus < 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 256;
+    }
+    cus = n > 0 ? n : 256;
+  }
+  return cus;
+}
+
+// K splits: only the store / residual epilogues split, when the tile grid leaves CUs idle; as
+// many as keep the grid within one workgroup per CU (a grid a little past that puts two on some
+// CUs, which then set the kernel's time: measured at 256 rows, 288 / 280-workgroup grids 9.09 ms
+// per verify forward, the same GEMMs split to 192 / 240 workgroups 8.15 ms, to 480 8.72 ms), and
+// at least 4 stages per split
 int gemm_tile_splits(int64_t M, int64_t N, int64_t K, int epi) {
   if (epi != EPI_NONE && epi != EPI_RES) return 1;
   const int64_t tiles = (M + TM - 1) / TM * tile_nblocks(N, epi);
   if (tiles >= 160) return 1;
-  int64_t sp = (256 + tiles - 1) / tiles;
+  int64_t sp = tile_cus() / tiles;
   const int64_t maxsp = (K / TK) / 4;
   if (sp > maxsp) sp = maxsp;
   return sp < 1 ? 1 : (int)sp;
