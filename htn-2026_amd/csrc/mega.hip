@@ -9,17 +9,23 @@
 // order and, before it waits for a phase's input, issues the loads of that phase's weight rows
 // (which never depend on the input), so HBM keeps streaming weights across phase boundaries.
 //
-// Cross-workgroup hand-off without fences: every produced vector element travels in a 64-bit
-// word {payload (32 bits), tag (32 bits)} written with one agent-scope relaxed atomic store and
-// read with agent-scope relaxed atomic loads (single-copy atomic, coherent across the XCDs'
-// L2s).  A consumer sees either the old word or the whole new one; it waits until the tag
-// equals this launch's tag.  Tags are epoch + 1, where the epoch (a word in the workspace) is
-// read by every workgroup at the start and advanced by workgroup 0 at the very end, after
-// every other workgroup has delivered its LM-head partial (which depends on everything it
-// read).  Every producer region is distinct per layer, so no word is rewritten in a launch.
+// Cross-workgroup hand-off without fences: every produced value travels in 32-bit words (two
+// bf16, or one fp32 / index) written with agent-scope relaxed atomic stores and read with
+// agent-scope relaxed atomic loads, mostly two words per load (single-copy atomic per word,
+// coherent across the XCDs' L2s).  A word holds its payload inverted (~payload), so 0 means
+// "not written yet": a consumer waits until every word it loaded is nonzero.  The one payload
+// whose inverse is 0, 0xFFFFFFFF (two bf16 NaNs, or an fp32 NaN), is stored as 0xFFFFFFFE, still
+// NaN.  The hand-off area has two copies that alternate with the parity of the epoch (a word in
+// the workspace, read by every workgroup at the start and advanced by workgroup 0 at the very
+// end, after every other workgroup has delivered its LM-head partial, which depends on
+// everything it read): a launch writes the copy of its parity, each word once, and zeroes the
+// other copy for the next launch, every workgroup its share, layer by layer.  Against a word of
+// {payload, 32-bit tag}, consumers load half the bytes.
 // Waits are bounded: after MG_SPIN_LIMIT polls, or once any wait has failed, a wait sets the
 // error word and returns; the launch then completes with garbage instead of hanging, and the
-// host reads the error word (qd_mega_ctl_offset) after the first replay.
+// host reads the error word (qd_mega_ctl_offset) after the first replay.  The workspace starts
+// zero-filled, and must be zero-filled again before a launch with another split plan (another
+// cap), which moves the words.
 //
 // Every workgroup is resident at once (grid = CU count, one 512-thread workgroup per CU,
 // checked against the occupancy API on the host), phases only wait on earlier phases, and
@@ -44,8 +50,8 @@ constexpr int H = 2560, INTER = 9728, HQ = 32, HKV = 8, HD = 128;
 constexpr int NQKV = (HQ + 2 * HKV) * HD;     // 6144
 constexpr int MIN_WG = 256;                   // rows per wave below assume >= 256 workgroups
 
-// LL region of one layer (words): the layer's input residual comes from the previous layer's
-// OUT (layer 0 reads the embedding row directly)
+// Hand-off words of one layer (32-bit words): the layer's input residual comes from the previous
+// layer's OUT (layer 0 reads the embedding row directly); offsets are even (8-byte aligned)
 struct Layout {
   int64_t qkv, att, mid, act, out, part, ml, per_layer, lm;
 };
@@ -71,29 +77,40 @@ struct MegaParams {
   int64_t *tok, *pos;
   bf16_t* x_out;       // final residual [H] (plain stores, for inspection)
   uint32_t* ctl;       // [0] epoch, [1] error
-  uint64_t* ll;
-  int64_t cap, chunk, vocab;
+  uint32_t* ll;        // two copies of `region` hand-off words
+  int64_t cap, chunk, vocab, region;
   int L, splits;
   float eps;
 };
 
-// ------------------------------------------------------------------ LL words
-__device__ __forceinline__ void ll_put(uint64_t* p, uint32_t payload, uint32_t tag) {
-  __hip_atomic_store(p, ((uint64_t)tag << 32) | payload, __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+// ------------------------------------------------------------------ hand-off words
+__device__ __forceinline__ uint32_t hw_enc(uint32_t payload) {
+  return ~(payload == 0xFFFFFFFFu ? 0xFFFFFFFEu : payload);
 }
-__device__ __forceinline__ uint64_t ll_raw(const uint64_t* p) {
+__device__ __forceinline__ void hw_put(uint32_t* p, uint32_t payload) {
+  __hip_atomic_store(p, hw_enc(payload), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// two words in one store (p 8-byte aligned)
+__device__ __forceinline__ void hw_put2(uint32_t* p, uint32_t lo, uint32_t hi) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), ((uint64_t)hw_enc(hi) << 32) | hw_enc(lo),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool hw_ready(uint32_t v) { return v != 0u; }
+__device__ __forceinline__ bool hw_ready(uint64_t v) {
+  return (uint32_t)v != 0u && (uint32_t)(v >> 32) != 0u;
+}
+// one word (uint32_t) or two (uint64_t, 8-byte aligned), as stored
+template <typename T>
+__device__ __forceinline__ T hw_raw(const T* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ bool ll_ready(uint64_t v, uint32_t tag) {
-  return (uint32_t)(v >> 32) == tag;
-}
 
-// Slow path of a wait: poll until the tag arrives; bounded, and a failed wait anywhere makes
-// every later wait give up within 64 polls.
-__device__ __noinline__ uint64_t ll_spin(const uint64_t* p, uint32_t tag, uint32_t* err) {
-  uint64_t v = ll_raw(p);
-  for (uint32_t it = 1; !ll_ready(v, tag); ++it) {
+// Slow path of a wait: poll until every word is written; bounded, and a failed wait anywhere
+// makes every later wait give up within 64 polls.
+template <typename T>
+__device__ __noinline__ T hw_spin(const T* p, uint32_t* err) {
+  T v = hw_raw(p);
+  for (uint32_t it = 1; !hw_ready(v); ++it) {
     if ((it & 63) == 0) {
       if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
       if (it >= MG_SPIN_LIMIT) {
@@ -102,42 +119,55 @@ __device__ __noinline__ uint64_t ll_spin(const uint64_t* p, uint32_t tag, uint32
       }
     }
     __builtin_amdgcn_s_sleep(1);
-    v = ll_raw(p);
+    v = hw_raw(p);
   }
   return v;
 }
 
-__device__ __forceinline__ uint32_t ll_wait(uint64_t v, const uint64_t* p, uint32_t tag,
-                                            uint32_t* err) {
-  if (!ll_ready(v, tag)) v = ll_spin(p, tag, err);
-  return (uint32_t)v;
+// the payload(s) of v, loaded from p, once written
+template <typename T>
+__device__ __forceinline__ T hw_wait(T v, const T* p, uint32_t* err) {
+  if (!hw_ready(v)) v = hw_spin(p, err);
+  return ~v;
 }
 
-// words [0, n) of src -> dst (LDS), WPT words per thread, all loads issued before any wait
+// zero this workgroup's share of words [0, n) (n even, dst 8-byte aligned)
+__device__ __forceinline__ void hw_clear(uint32_t* dst, int64_t n, int wg, int P) {
+  const int64_t a = (n / 2) * wg / P, b = (n / 2) * (wg + 1) / P;
+  uint64_t* d = reinterpret_cast<uint64_t*>(dst);
+  for (int64_t i = a + threadIdx.x; i < b; i += MG_NT)
+    __hip_atomic_store(d + i, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// words [0, n) of src -> dst (LDS); n even, src 8-byte aligned, n / 2 <= WPT * MG_NT; two words
+// per load, WPT loads per thread, all issued before any wait
 template <int WPT>
-__device__ __forceinline__ void ll_fetch_lds(const uint64_t* src, int n, uint32_t tag,
-                                             uint32_t* err, uint32_t* dst) {
+__device__ __forceinline__ void ll_fetch_lds(const uint32_t* src, int n, uint32_t* err,
+                                             uint32_t* dst) {
+  const uint64_t* s2 = reinterpret_cast<const uint64_t*>(src);
+  uint64_t* d2 = reinterpret_cast<uint64_t*>(dst);
+  const int np = n / 2;
   uint64_t v[WPT];
 #pragma unroll
   for (int j = 0; j < WPT; ++j) {
     const int idx = threadIdx.x + j * MG_NT;
-    v[j] = idx < n ? ll_raw(src + idx) : 0;
+    v[j] = idx < np ? hw_raw(s2 + idx) : 0;
   }
-  // A word still stale here was most likely written while the loads were in flight, and so
-  // were the thread's other stale words: once the first one has arrived, re-issue all of them
-  // together (one round trip) instead of polling them one after the other.
-  if (WPT > 1 && threadIdx.x < n && !ll_ready(v[0], tag)) {
-    v[0] = ll_spin(src + threadIdx.x, tag, err);
+  // A pair still unwritten here was most likely written while the loads were in flight, and so
+  // were the thread's other unwritten pairs: once the first one has arrived, re-issue all of
+  // them together (one round trip) instead of polling them one after the other.
+  if (WPT > 1 && threadIdx.x < np && !hw_ready(v[0])) {
+    v[0] = hw_spin(s2 + threadIdx.x, err);
 #pragma unroll
     for (int j = 1; j < WPT; ++j) {
       const int idx = threadIdx.x + j * MG_NT;
-      if (idx < n && !ll_ready(v[j], tag)) v[j] = ll_raw(src + idx);
+      if (idx < np && !hw_ready(v[j])) v[j] = hw_raw(s2 + idx);
     }
   }
 #pragma unroll
   for (int j = 0; j < WPT; ++j) {
     const int idx = threadIdx.x + j * MG_NT;
-    if (idx < n) dst[idx] = ll_wait(v[j], src + idx, tag, err);
+    if (idx < np) d2[idx] = hw_wait(v[j], s2 + idx, err);
   }
 }
 
@@ -225,21 +255,20 @@ struct Smem {
   DecodeAttnLds<ATTN_NW> attn;
 };
 
-// the workgroup's outputs obuf[0, nrows) -> LL words [w0, w0 + nrows / 2) of dst
-__device__ __forceinline__ void put_pairs(Smem& sm, uint64_t* dst, int64_t w0, int nrows,
-                                          uint32_t tag) {
+// the workgroup's outputs obuf[0, nrows) -> hand-off words [w0, w0 + nrows / 2) of dst
+__device__ __forceinline__ void put_pairs(Smem& sm, uint32_t* dst, int64_t w0, int nrows) {
   const int t = threadIdx.x;
   if (t < nrows / 2)
-    ll_put(dst + w0 + t, (uint32_t)sm.obuf[2 * t] | ((uint32_t)sm.obuf[2 * t + 1] << 16), tag);
+    hw_put(dst + w0 + t, (uint32_t)sm.obuf[2 * t] | ((uint32_t)sm.obuf[2 * t + 1] << 16));
 }
 
 // ------------------------------------------------------------------ phases
 // qkv = RMSNorm(x; ln1) . Wqkv^T   (rows wave, wave + 8, wave + 16 of the workgroup's 24)
-__device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t tag,
+__device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t* ll,
                           int64_t tok) {
   const int wave = threadIdx.x >> 6;
   const Layout ly = ll_layout(p.L, p.splits);
-  uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
+  uint32_t* LL = ll + (int64_t)l * ly.per_layer;
   int64_t a, b;
   part_range(NQKV / 2, wg, P, a, b);
   const int64_t r0 = 2 * a;
@@ -256,8 +285,8 @@ __device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, u
     const uint4* src = reinterpret_cast<const uint4*>(p.embed + (ok ? tok : 0) * H);
     for (int c = threadIdx.x; c < H / 8; c += MG_NT) sm.xs[c] = ok ? src[c] : make_uint4(0, 0, 0, 0);
   } else {
-    const uint64_t* prev = p.ll + (int64_t)(l - 1) * ly.per_layer + ly.out;
-    ll_fetch_lds<3>(prev, H / 2, tag, p.ctl + 1, xs32);
+    const uint32_t* prev = ll + (int64_t)(l - 1) * ly.per_layer + ly.out;
+    ll_fetch_lds<2>(prev, H / 2, p.ctl + 1, xs32);
   }
   lds_barrier();
   {                                // residual values of this workgroup's o rows
@@ -276,29 +305,29 @@ __device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, u
     }
   }
   lds_barrier();
-  put_pairs(sm, LL + ly.qkv, a, nr, tag);
+  put_pairs(sm, LL + ly.qkv, a, nr);
 }
 
 // one decode-attention unit (KV head, split) of layer l
-__device__ void phase_attn_unit(const MegaParams& p, Smem& sm, int l, int unit, uint32_t tag,
+__device__ void phase_attn_unit(const MegaParams& p, Smem& sm, int l, int unit, uint32_t* ll,
                                 int64_t pos) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const Layout ly = ll_layout(p.L, p.splits);
-  uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
+  uint32_t* LL = ll + (int64_t)l * ly.per_layer;
   const int kvh = unit / p.splits, split = unit % p.splits;
   const int64_t layer_kv = (int64_t)HKV * p.cap * HD;
   uint32_t* err = p.ctl + 1;
-  const uint64_t* qkv = LL + ly.qkv;
+  const uint32_t* qkv = LL + ly.qkv;
   auto fetch = [&](HeadVals& hv) -> int64_t {
     // element e of the packed qkv row lives in word e / 2, half e & 1; the unit's waves read
     // their q and k (v) rows in straight-line code, the other waves nothing
     if (wave < ATTN_NW) {
       const int64_t eq = attn_q_elem(wave, kvh), ek = attn_kv_elem<ATTN_NW>(wave, kvh, HQ, HKV);
-      const uint64_t* wq1 = qkv + ((eq + lane) >> 1);
-      const uint64_t* wq2 = qkv + ((eq + lane + 64) >> 1);
-      const uint64_t* wk1 = qkv + ((ek + lane) >> 1);
-      const uint64_t* wk2 = qkv + ((ek + lane + 64) >> 1);
-      const uint64_t rq1 = ll_raw(wq1), rq2 = ll_raw(wq2), rk1 = ll_raw(wk1), rk2 = ll_raw(wk2);
+      const uint32_t* wq1 = qkv + ((eq + lane) >> 1);
+      const uint32_t* wq2 = qkv + ((eq + lane + 64) >> 1);
+      const uint32_t* wk1 = qkv + ((ek + lane) >> 1);
+      const uint32_t* wk2 = qkv + ((ek + lane + 64) >> 1);
+      const uint32_t rq1 = hw_raw(wq1), rq2 = hw_raw(wq2), rk1 = hw_raw(wk1), rk2 = hw_raw(wk2);
       const bf16_t* qn = p.q_norm + (int64_t)l * HD;
       const bf16_t* kn = p.k_norm + (int64_t)l * HD;
       hv.qw1 = bf2f(qn[lane]); hv.qw2 = bf2f(qn[lane + 64]);
@@ -306,24 +335,21 @@ __device__ void phase_attn_unit(const MegaParams& p, Smem& sm, int l, int unit, 
       hv.c1 = bf2f(p.cos[pos * HD + lane]); hv.c2 = bf2f(p.cos[pos * HD + lane + 64]);
       hv.s1 = bf2f(p.sin[pos * HD + lane]); hv.s2 = bf2f(p.sin[pos * HD + lane + 64]);
       const uint32_t sh = (lane & 1) * 16;
-      hv.q1 = (ll_wait(rq1, wq1, tag, err) >> sh) & 0xFFFF;
-      hv.q2 = (ll_wait(rq2, wq2, tag, err) >> sh) & 0xFFFF;
-      hv.k1 = (ll_wait(rk1, wk1, tag, err) >> sh) & 0xFFFF;
-      hv.k2 = (ll_wait(rk2, wk2, tag, err) >> sh) & 0xFFFF;
+      hv.q1 = (hw_wait(rq1, wq1, err) >> sh) & 0xFFFF;
+      hv.q2 = (hw_wait(rq2, wq2, err) >> sh) & 0xFFFF;
+      hv.k1 = (hw_wait(rk1, wk1, err) >> sh) & 0xFFFF;
+      hv.k2 = (hw_wait(rk2, wk2, err) >> sh) & 0xFFFF;
     }
     return pos;
   };
   auto final_out = [&](int h, int d, float y0, float y1) {
-    ll_put(LL + ly.att + ((int64_t)(kvh * GRP + h) * HD + d) / 2, pack2(y0, y1), tag);
+    hw_put(LL + ly.att + ((int64_t)(kvh * GRP + h) * HD + d) / 2, pack2(y0, y1));
   };
   auto partial_out = [&](int h, int d, float A0, float A1, float M, float Lsum) {
     const int64_t idx = (int64_t)(kvh * GRP + h) * p.splits + split;
-    ll_put(LL + ly.part + idx * HD + d, __float_as_uint(A0), tag);
-    ll_put(LL + ly.part + idx * HD + d + 1, __float_as_uint(A1), tag);
-    if ((threadIdx.x & 63) == 0) {
-      ll_put(LL + ly.ml + idx * 2, __float_as_uint(M), tag);
-      ll_put(LL + ly.ml + idx * 2 + 1, __float_as_uint(Lsum), tag);
-    }
+    hw_put2(LL + ly.part + idx * HD + d, __float_as_uint(A0), __float_as_uint(A1));
+    if ((threadIdx.x & 63) == 0)
+      hw_put2(LL + ly.ml + idx * 2, __float_as_uint(M), __float_as_uint(Lsum));
   };
   decode_attn_unit<ATTN_NW>(sm.attn, fetch, final_out, partial_out,
                           p.k_cache + (int64_t)l * layer_kv, p.v_cache + (int64_t)l * layer_kv,
@@ -332,41 +358,33 @@ __device__ void phase_attn_unit(const MegaParams& p, Smem& sm, int l, int unit, 
 }
 
 // LSE merge of q head hq's split partials (one wave) -> ATT words of the head
-__device__ void phase_merge(const MegaParams& p, int l, int hq, uint32_t tag) {
+__device__ void phase_merge(const MegaParams& p, int l, int hq, uint32_t* ll) {
   const int lane = threadIdx.x & 63;
   const Layout ly = ll_layout(p.L, p.splits);
-  uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
+  uint32_t* LL = ll + (int64_t)l * ly.per_layer;
   uint32_t* err = p.ctl + 1;
   const int S = p.splits;
-  const uint64_t* ml = LL + ly.ml + (int64_t)hq * S * 2;
-  const uint64_t* acc = LL + ly.part + (int64_t)hq * S * HD + 2 * lane;
+  // (M, sum) of split sp, and the two accumulator values of this lane: one 8-byte pair each
+  const uint64_t* ml = reinterpret_cast<const uint64_t*>(LL + ly.ml + (int64_t)hq * S * 2);
+  const uint64_t* acc =
+      reinterpret_cast<const uint64_t*>(LL + ly.part + (int64_t)hq * S * HD + 2 * lane);
+  auto f2 = [](uint64_t v) {
+    return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+  };
   const float2 y = merge_splits(
       S,
-      [&](int sp) {
-        const uint64_t r0 = ll_raw(ml + 2 * sp), r1 = ll_raw(ml + 2 * sp + 1);
-        return make_float2(__uint_as_float(ll_wait(r0, ml + 2 * sp, tag, err)),
-                           __uint_as_float(ll_wait(r1, ml + 2 * sp + 1, tag, err)));
-      },
+      [&](int sp) { return f2(hw_wait(hw_raw(ml + sp), ml + sp, err)); },
       [&](int first, int n, float2 (&a)[MERGE_BATCH]) {
-        uint64_t r[MERGE_BATCH][2];
+        uint64_t r[MERGE_BATCH];
 #pragma unroll
         for (int q = 0; q < MERGE_BATCH; ++q)
-          if (q < n) {
-            r[q][0] = ll_raw(acc + (int64_t)(first + q) * HD);
-            r[q][1] = ll_raw(acc + (int64_t)(first + q) * HD + 1);
-          }
+          if (q < n) r[q] = hw_raw(acc + (int64_t)(first + q) * (HD / 2));
 #pragma unroll
-        for (int q = 0; q < MERGE_BATCH; ++q) {
-          if (q < n) {
-            const uint64_t* w0 = acc + (int64_t)(first + q) * HD;
-            a[q] = make_float2(__uint_as_float(ll_wait(r[q][0], w0, tag, err)),
-                               __uint_as_float(ll_wait(r[q][1], w0 + 1, tag, err)));
-          } else {
-            a[q] = make_float2(0.f, 0.f);
-          }
-        }
+        for (int q = 0; q < MERGE_BATCH; ++q)
+          a[q] = q < n ? f2(hw_wait(r[q], acc + (int64_t)(first + q) * (HD / 2), err))
+                       : make_float2(0.f, 0.f);
       });
-  ll_put(LL + ly.att + (int64_t)hq * (HD / 2) + lane, pack2(y.x, y.y), tag);
+  hw_put(LL + ly.att + (int64_t)hq * (HD / 2) + lane, pack2(y.x, y.y));
 }
 
 // mid = x + bf16(attn . Wo^T)   (the workgroup's o rows, o_rows: row wave + 8 rr), then
@@ -376,10 +394,10 @@ __device__ void phase_merge(const MegaParams& p, int l, int hq, uint32_t tag) {
 // attention hand-offs; the third after the o rows are consumed, so it streams during the MID
 // hand-off; later act rows refill the 3-slot ring as rows are consumed.  A workgroup without o
 // rows skips the attention output and goes straight to the MID wait.
-__device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t tag) {
+__device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t* ll) {
   const int wave = threadIdx.x >> 6;
   const Layout ly = ll_layout(p.L, p.splits);
-  uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
+  uint32_t* LL = ll + (int64_t)l * ly.per_layer;
   int64_t a, b;
   o_rows(p, wg, P, a, b);
   const int64_t r0 = 2 * a;
@@ -405,7 +423,7 @@ __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, 
   load_gu(0, 0);
   load_gu(1, 1);
   if (nr > 0) {                    // uniform over the workgroup
-    ll_fetch_lds<4>(LL + ly.att, HQ * HD / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
+    ll_fetch_lds<2>(LL + ly.att, HQ * HD / 2, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
     lds_barrier();
 #pragma unroll
     for (int rr = 0; rr < 3; ++rr) {
@@ -416,12 +434,12 @@ __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, 
       }
     }
     lds_barrier();
-    put_pairs(sm, LL + ly.mid, a, nr, tag);
+    put_pairs(sm, LL + ly.mid, a, nr);
   }
   load_gu(2, 2);                   // streams during the MID hand-off
   const uint4 nw = mg_norm_w<5>(p.ln2 + (int64_t)l * H);
   // ---- gate/up + SwiGLU
-  ll_fetch_lds<3>(LL + ly.mid, H / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
+  ll_fetch_lds<2>(LL + ly.mid, H / 2, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
   lds_barrier();
   {                                // residual values of this workgroup's down rows
     int64_t da, db;
@@ -442,14 +460,16 @@ __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, 
     }
   }
   lds_barrier();
-  put_pairs(sm, LL + ly.act, ga, ng, tag);
+  put_pairs(sm, LL + ly.act, ga, ng);
 }
 
-// out = mid + bf16(act . Wdown^T)   (10 rows as phase_o)
-__device__ void phase_down(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t tag) {
+// out = mid + bf16(act . Wdown^T)   (10 rows as phase_o); with the weights in flight, the
+// workgroup zeroes its share of layer l's words in the other copy (nxt)
+__device__ void phase_down(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t* ll,
+                           uint32_t* nxt) {
   const int wave = threadIdx.x >> 6;
   const Layout ly = ll_layout(p.L, p.splits);
-  uint64_t* LL = p.ll + (int64_t)l * ly.per_layer;
+  uint32_t* LL = ll + (int64_t)l * ly.per_layer;
   int64_t a, b;
   part_range(H / 2, wg, P, a, b);
   const int64_t r0 = 2 * a;
@@ -459,7 +479,8 @@ __device__ void phase_down(const MegaParams& p, Smem& sm, int l, int wg, int P, 
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr)
     if (wave + rr * MG_NW < nr) mg_load_row<19>(W, r0 + wave + rr * MG_NW, w[rr]);
-  ll_fetch_lds<10>(LL + ly.act, INTER / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
+  hw_clear(nxt + (int64_t)l * ly.per_layer, ly.per_layer, wg, P);
+  ll_fetch_lds<5>(LL + ly.act, INTER / 2, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
   lds_barrier();
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
@@ -470,13 +491,15 @@ __device__ void phase_down(const MegaParams& p, Smem& sm, int l, int wg, int P, 
     }
   }
   lds_barrier();
-  put_pairs(sm, LL + ly.out, a, nr, tag);
+  put_pairs(sm, LL + ly.out, a, nr);
   if (l == p.L - 1 && threadIdx.x < nr) p.x_out[r0 + threadIdx.x] = sm.obuf[threadIdx.x];
 }
 
 // final RMSNorm + LM head over the workgroup's vocab rows: best (bf16 logit, lowest index)
-// -> 2 LL words; four rows in flight per wave
-__device__ void phase_lm(const MegaParams& p, Smem& sm, int wg, int P, uint32_t tag) {
+// -> 2 hand-off words (and the same two words of the other copy zeroed); four rows in flight
+// per wave
+__device__ void phase_lm(const MegaParams& p, Smem& sm, int wg, int P, uint32_t* ll,
+                         uint32_t* nxt) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const Layout ly = ll_layout(p.L, p.splits);
   int64_t r0, r1;
@@ -487,8 +510,8 @@ __device__ void phase_lm(const MegaParams& p, Smem& sm, int wg, int P, uint32_t 
   for (int s = 0; s < 4; ++s)
     if (wave + s * MG_NW < nr) mg_load_row<5>(p.embed, r0 + wave + s * MG_NW, buf[s]);
   const uint4 nw = mg_norm_w<5>(p.final_norm);
-  const uint64_t* last = p.ll + (int64_t)(p.L - 1) * ly.per_layer + ly.out;
-  ll_fetch_lds<3>(last, H / 2, tag, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
+  const uint32_t* last = ll + (int64_t)(p.L - 1) * ly.per_layer + ly.out;
+  ll_fetch_lds<2>(last, H / 2, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
   lds_barrier();
   mg_norm<5, 256>(sm.xs, nw, p.eps, sm.red);
   float bv = -INFINITY;
@@ -515,23 +538,24 @@ __device__ void phase_lm(const MegaParams& p, Smem& sm, int wg, int P, uint32_t 
       const int32_t i2 = sm.best_i[q];
       if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
     }
-    ll_put(p.ll + ly.lm + 2 * wg, __float_as_uint(v), tag);
-    ll_put(p.ll + ly.lm + 2 * wg + 1, (uint32_t)i, tag);
+    hw_put2(ll + ly.lm + 2 * wg, __float_as_uint(v), (uint32_t)i);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(nxt + ly.lm + 2 * wg), (uint64_t)0,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 // workgroup 0: global (max, lowest index) over the partials -> tok; pos += 1; epoch += 1
-__device__ void phase_final(const MegaParams& p, Smem& sm, int P, uint32_t tag, uint32_t epoch,
+__device__ void phase_final(const MegaParams& p, Smem& sm, int P, uint32_t* ll, uint32_t epoch,
                             int64_t pos) {
   const Layout ly = ll_layout(p.L, p.splits);
-  const uint64_t* lm = p.ll + ly.lm;
+  const uint64_t* lm = reinterpret_cast<const uint64_t*>(ll + ly.lm);
   uint32_t* err = p.ctl + 1;
   float bv = -INFINITY;
   int32_t bi = 0x7FFFFFFF;
   for (int q = threadIdx.x; q < P; q += MG_NT) {
-    const uint64_t r0 = ll_raw(lm + 2 * q), r1 = ll_raw(lm + 2 * q + 1);
-    const float v = __uint_as_float(ll_wait(r0, lm + 2 * q, tag, err));
-    const int32_t i = (int32_t)ll_wait(r1, lm + 2 * q + 1, tag, err);
+    const uint64_t r = hw_wait(hw_raw(lm + q), lm + q, err);
+    const float v = __uint_as_float((uint32_t)r);
+    const int32_t i = (int32_t)(uint32_t)(r >> 32);
     if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
   }
   // wave argmax, then across waves
@@ -563,7 +587,8 @@ __global__ __launch_bounds__(MG_NT) void mega_step_kernel(MegaParams p) {
   const int wg = blockIdx.x, P = gridDim.x;
   const int wave = threadIdx.x >> 6;
   const uint32_t epoch = __hip_atomic_load(p.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t tag = epoch + 1;
+  uint32_t* ll = p.ll + (int64_t)(epoch & 1u) * p.region;          // this launch's words
+  uint32_t* nxt = p.ll + (int64_t)((epoch & 1u) ^ 1u) * p.region;   // the next launch's
   const int64_t pos = p.pos[0];
   const int64_t tok = p.tok[0];
   if (pos < 0 || pos >= p.cap) {   // uniform over the grid: nothing is written, nobody waits
@@ -574,14 +599,14 @@ __global__ __launch_bounds__(MG_NT) void mega_step_kernel(MegaParams p) {
   const int units = HKV * p.splits;
   const int merge0 = P - HQ;       // workgroups merge0 .. P-1 merge one q head each
   for (int l = 0; l < p.L; ++l) {
-    phase_qkv(p, sm, l, wg, P, tag, tok);
-    for (int u = wg; u < units; u += P) phase_attn_unit(p, sm, l, u, tag, pos);
-    if (p.splits > 1 && wg >= merge0 && wave == 0) phase_merge(p, l, wg - merge0, tag);
-    phase_o_gu(p, sm, l, wg, P, tag);
-    phase_down(p, sm, l, wg, P, tag);
+    phase_qkv(p, sm, l, wg, P, ll, tok);
+    for (int u = wg; u < units; u += P) phase_attn_unit(p, sm, l, u, ll, pos);
+    if (p.splits > 1 && wg >= merge0 && wave == 0) phase_merge(p, l, wg - merge0, ll);
+    phase_o_gu(p, sm, l, wg, P, ll);
+    phase_down(p, sm, l, wg, P, ll, nxt);
   }
-  phase_lm(p, sm, wg, P, tag);
-  if (wg == 0) phase_final(p, sm, P, tag, epoch, pos);
+  phase_lm(p, sm, wg, P, ll, nxt);
+  if (wg == 0) phase_final(p, sm, P, ll, epoch, pos);
 }
 
 }  // namespace
@@ -608,9 +633,14 @@ bool mega_shape_ok(int hidden, int inter, int hq, int hkv, int head_dim) {
   return hidden == H && inter == INTER && hq == HQ && hkv == HKV && head_dim == HD;
 }
 
-int64_t mega_ll_bytes(int L, int64_t splits, int grid) {
+// words of one copy of the hand-off area (a multiple of 64: each copy 256-byte aligned)
+static int64_t ll_region_words(int L, int64_t splits, int grid) {
   const Layout ly = ll_layout(L, splits);
-  return (ly.lm + 2 * (int64_t)grid) * 8;
+  return (ly.lm + 2 * (int64_t)grid + 63) / 64 * 64;
+}
+
+int64_t mega_ll_bytes(int L, int64_t splits, int grid) {
+  return 2 * ll_region_words(L, splits, grid) * 4;
 }
 
 int64_t mega_splits(int64_t cap) { return decode_attn_splits(1, HKV, cap); }
@@ -626,6 +656,7 @@ hipError_t launch_mega_step(const MegaLaunch& m, hipStream_t s) {
   p.chunk = decode_attn_chunk(m.cap, p.splits);
   const int grid = mega_grid();
   if (grid <= 0) return hipErrorInvalidConfiguration;
+  p.region = ll_region_words(m.L, p.splits, grid);
   mega_step_kernel<<<dim3((unsigned)grid), dim3(MG_NT), 0, s>>>(p);
   return hipGetLastError();
 }

@@ -405,7 +405,7 @@ int qd_mega_step(const qd_weights* w, const qd_decode_state* st, void* stream) {
   m.q_norm = w->q_norm; m.k_norm = w->k_norm; m.cos = st->cos; m.sin = st->sin;
   m.k_cache = st->k_cache; m.v_cache = st->v_cache; m.tok = st->tok; m.pos = st->pos;
   m.x_out = st->x; m.ctl = reinterpret_cast<uint32_t*>(ws + off);
-  m.ll = reinterpret_cast<uint64_t*>(ws + off + 256);
+  m.ll = reinterpret_cast<uint32_t*>(ws + off + 256);
   m.cap = st->cap; m.vocab = w->vocab; m.L = w->n_layers; m.eps = w->eps;
   const hipError_t e = launch_mega_step(m, S(stream));
   return e == hipSuccess ? QD_OK : (int)e;

@@ -84,7 +84,7 @@ struct MegaLaunch {
   int64_t *tok, *pos;
   bf16_t* x_out;
   uint32_t* ctl;        // [0] epoch, [1] error; zero before the first launch
-  uint64_t* ll;         // mega_ll_bytes, zero before the first launch
+  uint32_t* ll;         // mega_ll_bytes, zero before the first launch with this split plan
   int64_t cap, vocab;
   int L;
   float eps;

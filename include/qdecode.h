@@ -174,11 +174,13 @@ int64_t qd_decode_workspace_bytes(const qd_weights *w, int64_t batch, int64_t ca
 int qd_decode_step(const qd_weights *w, const qd_decode_state *st, void *stream);
 
 /* The same step (batch == 1) as ONE persistent launch of one workgroup per CU that hands
- * activations between phases through tagged 64-bit words instead of launch boundaries.
+ * activations between phases through hand-off words in the workspace instead of launch
+ * boundaries.
  * Replaces the T6 tier (engine/kernels/mega.py:1-15, MegaStep; used at engine/engine.py:596-597).
  * Bit-identical to qd_decode_step at batch 1 (tokens, K/V, st->x = final residual; st->qkv,
  * st->attn and st->act are not written).  Needs a workspace of qd_mega_workspace_bytes (which
- * also covers qd_decode_step's), zero-filled once before the first step; the 32-bit word at
+ * also covers qd_decode_step's), zero-filled before the first step and again before a step
+ * with a different cap (the hand-off words move with the attention split plan); the 32-bit word at
  * byte qd_mega_ctl_offset of it is the step epoch and the next one the error word: 0 = ok,
  * 1 = a hand-off wait expired (the step's results are invalid), 2 = pos outside [0, cap)
  * (nothing written).  The error word stays set until the caller clears it.
