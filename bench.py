@@ -224,6 +224,50 @@ def time_gu_kernel(eng, sh, reps=20):
     return us, nbytes
 
 
+def time_read_ceiling(eng, reps=20, grids=(768, 2048, 4864)):
+    """The read rate one launch can reach over the gate/up GEMV's weight bytes: qd_read_probe
+    (non-temporal 16-byte loads, nothing computed or written) over the same 36 layers'
+    W_gate|W_up, captured as one hipGraph of 36 launches like time_gu_kernel and replayed; the
+    best of three grids.  Returns (us per launch, grid, bytes per launch)."""
+    import ctypes as C
+
+    import torch
+    from qdecode import _lib
+    m, st = eng.model, eng.stream
+    sink = torch.zeros(1, dtype=torch.int32, device=m.device)
+    nbytes = m.w_gu[0].numel() * m.w_gu[0].element_size()
+    best = None
+    for g in grids:
+        with torch.cuda.stream(st):
+            _lib.call("qd_graph_begin", st.cuda_stream)
+            try:
+                for l in range(m.L):
+                    w = m.w_gu[l]
+                    assert w.is_contiguous() and w.numel() * w.element_size() == nbytes
+                    _lib.call("qd_read_probe", w.data_ptr(), nbytes, g, sink.data_ptr(),
+                              st.cuda_stream)
+            finally:
+                ex = C.c_void_p()
+                rc = _lib.LIB.qd_graph_end(st.cuda_stream, C.byref(ex))
+            if rc != 0:
+                raise _lib.QDError("qd_graph_end", rc)
+            for _ in range(2):
+                _lib.call("qd_graph_launch", ex, st.cuda_stream)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(st):
+            e0.record(st)
+            for _ in range(reps):
+                _lib.call("qd_graph_launch", ex, st.cuda_stream)
+            e1.record(st)
+        torch.cuda.synchronize()
+        _lib.LIB.qd_graph_destroy(ex)
+        us = e0.elapsed_time(e1) * 1e3 / (reps * m.L)
+        if best is None or us < best[0]:
+            best = (us, g)
+    return best[0], best[1], nbytes
+
+
 def layer_kernels(reps=1000):
     """Config 2: the fused layer kernels on their own, B in {1, 8, 64}, synthetic bf16 N(0, 1)
     activations, positions uniform on [0, 8192).  Each kernel is captured `reps` times into one
@@ -382,6 +426,9 @@ def main():
         f"{r1['achieved_gbs']:.0f} GB/s, prefill {r1['prefill_s']:.2f}s")
     us, gu_bytes = time_gu_kernel(eng, sh)
     log(f"gate/up GEMV: {us:.2f} us/launch, {gu_bytes / (us * 1e-6) / 1e9:.0f} GB/s")
+    ceil_us, ceil_grid, ceil_bytes = time_read_ceiling(eng)
+    log(f"read ceiling over the same weights: {ceil_us:.2f} us/launch, "
+        f"{ceil_bytes / (ceil_us * 1e-6) / 1e9:.0f} GB/s (grid {ceil_grid})")
 
     layer = None
     if not a.no_layer:
@@ -437,7 +484,13 @@ def main():
     gemv = {"bound": "hbm", "kernel": "gemv_kernel gate/up + SwiGLU (B=1, per-launch step)",
             "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": GU_TRAFFIC_B1,
-            "bytes_per_launch": gu_bytes, "us_per_launch": round(us, 3)}
+            "bytes_per_launch": gu_bytes, "us_per_launch": round(us, 3),
+            # qd_read_probe over the same weight bytes: what one launch of this size can read
+            "read_ceiling": {"us_per_launch": round(ceil_us, 3), "grid": ceil_grid,
+                             "bytes_per_launch": ceil_bytes,
+                             "achieved": round(ceil_bytes / (ceil_us * 1e-6) / 1e9, 1),
+                             "frac": round(ceil_bytes / (ceil_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)},
+            "of_read_ceiling": round(ceil_us / us, 4)}
     if r1["mega"]:
         roofline = {"bound": "hbm", "kernel": "mega_step_kernel (whole B=1 decode step)",
                     "achieved": round(r1["achieved_gbs"], 1), "peak": PEAK_HBM_GBS,

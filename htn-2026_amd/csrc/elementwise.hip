@@ -345,6 +345,31 @@ void launch_fill(bf16_t* out, int64_t count, uint16_t value, hipStream_t s) {
   fill_kernel<<<dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s>>>(out, count, value);
 }
 
+// ------------------------------------------------------------------ read-stream probe
+// Reads n 16-byte chunks with non-temporal loads, grid-stride, four loads in flight per thread,
+// folded into one word that is stored only if it equals a constant no data here produces (so
+// the loads are not optimised away and nothing is written): the single-launch read rate the
+// memory system gives a kernel of this size, the bound for any kernel that reads these bytes.
+__global__ __launch_bounds__(256) void read_probe_kernel(const uint4* __restrict__ p, int64_t n,
+                                                         uint32_t* sink) {
+  int64_t i = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * 1024;
+  uint32_t acc = 0;
+  for (; i < n; i += stride) {
+    uint4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = i + u * 256 < n ? ld_stream(p + i + u * 256) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  if (acc == 0x5EEDF00Du) sink[0] = acc;
+}
+
+void launch_read_probe(const void* buf, int64_t bytes, int grid, uint32_t* sink, hipStream_t s) {
+  read_probe_kernel<<<dim3((unsigned)grid), dim3(256), 0, s>>>(static_cast<const uint4*>(buf),
+                                                               bytes / 16, sink);
+}
+
 // ------------------------------------------------------------------ greedy argmax reduction
 // tok[m] = index of the maximum over the per-tile (value, lowest index) partials of row m,
 // lowest index on exact ties (gemv.py:147-154, fast.py:402-426); optionally pos[0] += 1.

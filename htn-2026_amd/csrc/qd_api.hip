@@ -293,6 +293,14 @@ int qd_fill_bf16(uint16_t* out, int64_t count, uint16_t value, void* stream) {
   return launched();
 }
 
+int qd_read_probe(const void* buf, int64_t bytes, int32_t grid, uint32_t* sink, void* stream) {
+  if (bytes < 0 || (bytes & 15) || grid < 1 || grid > 65536 || !sink) return QD_EARG;
+  if (bytes == 0) return QD_OK;
+  if (!buf || (reinterpret_cast<uintptr_t>(buf) & 15)) return QD_EARG;
+  launch_read_probe(buf, bytes, grid, sink, S(stream));
+  return launched();
+}
+
 // ------------------------------------------------------------------ decode step
 int64_t qd_decode_workspace_bytes(const qd_weights* w, int64_t batch, int64_t cap) {
   if (!w || batch <= 0 || cap <= 0) return 0;

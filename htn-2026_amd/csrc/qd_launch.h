@@ -34,6 +34,7 @@ void launch_kv_compact(bf16_t* k_all, bf16_t* v_all, int64_t L, int64_t B, int H
 void launch_synth(bf16_t* out, int64_t count, uint64_t seed, uint64_t stream, uint64_t start,
                   float scale, hipStream_t s);
 void launch_fill(bf16_t* out, int64_t count, uint16_t value, hipStream_t s);
+void launch_read_probe(const void* buf, int64_t bytes, int grid, uint32_t* sink, hipStream_t s);
 void launch_argmax_reduce(const float* pval, const int32_t* pidx, int64_t nparts, int64_t M,
                           int64_t* tok, int64_t* pos_inc, hipStream_t s);
 

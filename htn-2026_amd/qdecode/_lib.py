@@ -71,6 +71,7 @@ SIGNATURES = {
     "qd_kv_compact": ([p, p, i64, i64, i64, i64, p, p, p, i64, p], i32),
     "qd_synth_bf16": ([p, i64, u64, u64, u64, f32, p], i32),
     "qd_fill_bf16": ([p, i64, C.c_uint16, p], i32),
+    "qd_read_probe": ([p, i64, i32, p, p], i32),
     "qd_decode_workspace_bytes": ([C.POINTER(Weights), i64, i64], i64),
     "qd_decode_step": ([C.POINTER(Weights), C.POINTER(DecodeState), p], i32),
     "qd_mega_supported": ([C.POINTER(Weights), i64], i32),

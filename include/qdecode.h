@@ -133,6 +133,12 @@ int qd_synth_bf16(uint16_t *out, int64_t count, uint64_t seed, uint64_t stream, 
                   float scale, void *stream_);
 int qd_fill_bf16(uint16_t *out, int64_t count, uint16_t value, void *stream);
 
+/* Read-stream probe (no reference counterpart; the benchmark's measuring stick): reads `bytes`
+ * (a multiple of 16, buf 16-byte aligned) with non-temporal 16-byte loads from `grid`
+ * workgroups of 256 threads and writes nothing (sink is never written for real data).  Timed
+ * over the same bytes as a kernel, it gives the read rate one launch of that size can reach. */
+int qd_read_probe(const void *buf, int64_t bytes, int32_t grid, uint32_t *sink, void *stream);
+
 /* ------------------------------------------------------------------ whole steps */
 /* Stacked, packed weights as the reference lays them out (engine/engine.py:250-282). */
 typedef struct {

@@ -63,6 +63,12 @@ def test_argument_errors_without_device(lib):
                                None) == EWS
     assert L.qd_graph_begin(None) == EARG
     assert L.qd_graph_destroy(None) == 0
+    sink = C.c_void_p(256)
+    assert L.qd_read_probe(x, 1000, 64, sink, None) == EARG                         # bytes % 16
+    assert L.qd_read_probe(C.c_void_p(264), 1024, 64, sink, None) == EARG           # misaligned
+    assert L.qd_read_probe(x, 1024, 0, sink, None) == EARG                          # grid < 1
+    assert L.qd_read_probe(x, 1024, 64, None, None) == EARG                         # no sink
+    assert L.qd_read_probe(None, 0, 64, sink, None) == 0                            # nothing to read
 
 
 def test_workspace_sizes(lib):

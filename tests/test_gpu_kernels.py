@@ -373,3 +373,19 @@ def test_kv_compact(ops):
             ke[:, b, :, base[b] + kk] = ke[:, b, :, base[b] + s]
             ve[:, b, :, base[b] + kk] = ve[:, b, :, base[b] + s]
     assert torch.equal(k.cpu(), ke) and torch.equal(v.cpu(), ve)
+
+
+# ------------------------------------------------------------------ read-stream probe
+@pytest.mark.parametrize("nbytes,grid", [(16, 1), (1 << 20, 64), ((1 << 20) + 48, 4864)])
+def test_read_probe_reads_and_writes_nothing(nbytes, grid):
+    """qd_read_probe (the benchmark's read-ceiling kernel) runs over ragged sizes and grids
+    larger than the data, leaves its input untouched and never writes the sink for real data."""
+    from qdecode import _lib
+    say(f"read probe {nbytes} B, grid {grid}")
+    buf = torch.arange(nbytes // 2, dtype=torch.int16, device=DEV)
+    before = buf.clone()
+    sink = torch.full((1,), -7, dtype=torch.int32, device=DEV)
+    _lib.call("qd_read_probe", buf.data_ptr(), nbytes, grid, sink.data_ptr(),
+              torch.cuda.current_stream().cuda_stream)
+    sync()
+    assert int(sink.item()) == -7 and torch.equal(buf, before)
