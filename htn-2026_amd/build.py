@@ -19,7 +19,10 @@ ARCH = os.environ.get("QD_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall",
+    # a variable read inside its own initialiser (e.g. a macro local named like its argument)
+    # builds a garbage address: never let it through
+    "-Werror=uninitialized", "-Wno-unused-function",
     "-Wno-unused-variable", "-Wno-unused-but-set-variable",
     # packed fp32 forms are kept out of the generated code (see the build notes)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

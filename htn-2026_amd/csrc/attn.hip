@@ -116,6 +116,13 @@ int64_t decode_attn_chunk(int64_t cap, int64_t splits) {
   return (chunk + ATTN_TILE - 1) / ATTN_TILE * ATTN_TILE;
 }
 
+static void launch_decode_attn_mfma(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn,
+                                    const bf16_t* kn, const bf16_t* cos_t, const bf16_t* sin_t,
+                                    const int64_t* pos, bf16_t* k_cache, bf16_t* v_cache,
+                                    int64_t B, int Hq, int Hkv, int64_t cap, int64_t splits,
+                                    int64_t chunk, float eps, float* ws_acc, float* ws_ml,
+                                    bf16_t* out, bool rope_row, hipStream_t s);
+
 void launch_decode_attn(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn, const bf16_t* kn,
                         const bf16_t* cos_t, const bf16_t* sin_t, const int64_t* pos,
                         bf16_t* k_cache, bf16_t* v_cache, int64_t B, int Hq, int Hkv, int64_t cap,
@@ -123,7 +130,10 @@ void launch_decode_attn(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn,
                         bool rope_row, hipStream_t s) {
   const int64_t chunk = decode_attn_chunk(cap, splits);
   const dim3 grid((unsigned)splits, (unsigned)Hkv, (unsigned)B), block(ATTN_NW * 64);
-  if (rope_row)
+  if (B >= 2)
+    launch_decode_attn_mfma(qkv, qkv_stride, qn, kn, cos_t, sin_t, pos, k_cache, v_cache, B, Hq,
+                            Hkv, cap, splits, chunk, eps, ws_acc, ws_ml, out, rope_row, s);
+  else if (rope_row)
     decode_attn_kernel<ATTN_NW, true><<<grid, block, 0, s>>>(
         qkv, qkv_stride, qn, kn, cos_t, sin_t, pos, k_cache, v_cache, Hq, Hkv, cap, chunk, eps,
         1.0f / sqrtf(128.0f), ws_acc, ws_ml, out);
@@ -379,6 +389,268 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
 }
 
 // the most splits (BLOCK_CHUNK keys each) a launch may use: what the workspace is sized for
+// ------------------------------------------------------------------ decode attention on MFMA (B >= 2)
+// The decode unit (decode_attn_unit: same prologue, same numerics) with its two contractions on
+// v_mfma_f32_16x16x32_bf16.  Workgroup = (key split, KV head, sequence), 8 waves.  After the
+// prologue (q / k RMSNorm + RoPE, the new token's K/V written to the cache by the split that
+// owns pos), wave w takes tiles w, w + 8, ... of 32 keys of the split's range, the new token
+// included: it stages each tile key-major in its own LDS region (one 1 KiB-contiguous
+// non-temporal load per 4 keys, 16-byte units XOR-swizzled by key; the new token's row from
+// LDS) and contracts it as the block kernel does, with the group's 4 query heads as columns
+// 0..3 of the 16-column B operand: S' = K . Q^T, online softmax per column, O^T += V^T . P^T
+// with transposed V reads.  The waves' (m, l, O) are then combined in LDS (over the staging
+// region) and written exactly as the unit writes them (normalised output, or split partials
+// for attn_merge_kernel).  Measured at B = 32 (256 workgroups, ~2112 keys each): the VALU unit
+// takes 51.9 us per layer (VALU busy 77 % of its cycles); this kernel with 4 waves and plain
+// loads 51.0 us (the same whether one or two tiles are in flight per wave), with 8 waves
+// ~49.7 us, with the K/V loads non-temporal 45.0 us.  Agrees with decode_attn_kernel up to fp32
+// summation order; B = 1 keeps decode_attn_kernel, whose arithmetic the persistent step shares
+// bit for bit.
+constexpr int DM_NW = 8;
+
+struct DecodeMfmaLds {
+  union {
+    struct {
+      uint4 ks[DM_NW][32 * 16];   // each wave's staged K tile (32 keys x 16 units)
+      uint4 vs[DM_NW][32 * 16];
+    } t;
+    float wacc[DM_NW][GRP][128];  // after every wave's last tile: the waves' O
+  } u;
+  uint32_t qs[GRP][64];        // normalised q of the group's heads, packed bf16 pairs
+  uint32_t kns[64], vns[64];   // the new token's K (normalised) and V rows
+  float wm[DM_NW][GRP], wl[DM_NW][GRP];
+};
+
+template <bool ROPE_ROW>
+__global__ __launch_bounds__(DM_NW * 64) void decode_attn_mfma_kernel(
+    const bf16_t* __restrict__ qkv, int64_t qkv_stride, const bf16_t* __restrict__ qn,
+    const bf16_t* __restrict__ kn, const bf16_t* __restrict__ cos_t,
+    const bf16_t* __restrict__ sin_t, const int64_t* __restrict__ pos_ptr, bf16_t* k_cache,
+    bf16_t* v_cache, int Hq, int Hkv, int64_t cap, int64_t chunk, float eps, float scale,
+    float* ws_acc, float* ws_ml, bf16_t* out) {
+  typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+  typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+  // 16-byte units as a native vector: copies of HIP's uint4 struct are memcpys, which keep the
+  // staging arrays out of registers
+  typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+  __shared__ DecodeMfmaLds sm;
+  const int split = blockIdx.x, kvh = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int splits = gridDim.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = lane & 15, q4 = lane >> 4;
+  const int64_t head_off = ((b * Hkv + kvh) * cap) * 128;
+  const u4v* kb = reinterpret_cast<const u4v*>(k_cache + head_off);
+  const u4v* vb = reinterpret_cast<const u4v*>(v_cache + head_off);
+  const int64_t start = (int64_t)split * chunk;
+  // staging: lane moves 16-byte unit c of keys q4 + 4 j (j < 8) of a tile; keys at or past lim
+  // reload row lim - 1 (a valid row, never attended as such)
+  // one tile in flight per wave (registers), refilled as soon as the tile is staged
+  u4v kx[8], vx[8];
+#define DM_LD(KX, VX, J0, LIM)                                                 \
+  _Pragma("unroll") for (int dm_j_ = 0; dm_j_ < 8; ++dm_j_) {                  \
+    const int64_t dm_key_ = (J0) + q4 + 4 * dm_j_;                             \
+    const int64_t dm_row_ = dm_key_ < (LIM) ? dm_key_ : (LIM) - 1;             \
+    const int64_t dm_r_ = dm_row_ > 0 ? dm_row_ : 0;                           \
+    KX[dm_j_] = __builtin_nontemporal_load(kb + dm_r_ * 16 + c);               \
+    VX[dm_j_] = __builtin_nontemporal_load(vb + dm_r_ * 16 + c);               \
+  }
+  DM_LD(kx, vx, start + 32 * wave, cap);   // the wave's first tile, before pos is known
+  // prologue loads: q head kvh * 4 + wave (waves 0..3; the others load it too and drop it);
+  // wave 0 the new k, wave 1 the new v
+  const bf16_t* row = qkv + b * qkv_stride;
+  const bf16_t* qsrc = row + (int64_t)(kvh * GRP + (wave & (GRP - 1))) * 128;
+  const bf16_t* ksrc = row + (int64_t)(Hq + (wave == 1 ? Hkv : 0) + kvh) * 128;
+  const uint32_t q1 = qsrc[lane], q2 = qsrc[lane + 64];
+  const uint32_t k1 = ksrc[lane], k2 = ksrc[lane + 64];
+  const float qw1 = bf2f(qn[lane]), qw2 = bf2f(qn[lane + 64]);
+  const float kw1 = bf2f(kn[lane]), kw2 = bf2f(kn[lane + 64]);
+  float c1, c2, s1, s2;
+  if constexpr (ROPE_ROW) {
+    c1 = bf2f(cos_t[lane]); c2 = bf2f(cos_t[lane + 64]);
+    s1 = bf2f(sin_t[lane]); s2 = bf2f(sin_t[lane + 64]);
+  }
+  const int64_t pos = pos_ptr[0];
+  if constexpr (!ROPE_ROW) {
+    const int64_t pr = (pos >= 0 && pos < cap ? pos : 0) * 128;
+    c1 = bf2f(cos_t[pr + lane]); c2 = bf2f(cos_t[pr + lane + 64]);
+    s1 = bf2f(sin_t[pr + lane]); s2 = bf2f(sin_t[pr + lane + 64]);
+  }
+  if (pos < 0 || pos >= cap) return;   // uniform over the grid: no slot to write
+  const bool owns = pos >= start && pos < start + chunk;
+  const int64_t kend = owns ? pos + 1 : (start + chunk < pos ? start + chunk : pos);
+  if (wave < GRP) {
+    float o1, o2;
+    norm_rope_vals(bf2f(q1), bf2f(q2), qw1, qw2, c1, c2, s1, s2, eps, o1, o2);
+    reinterpret_cast<bf16_t*>(sm.qs[wave])[lane] = (bf16_t)f2bf(o1);
+    reinterpret_cast<bf16_t*>(sm.qs[wave])[lane + 64] = (bf16_t)f2bf(o2);
+  }
+  if (owns && wave == 0) {
+    float o1, o2;
+    norm_rope_vals(bf2f(k1), bf2f(k2), kw1, kw2, c1, c2, s1, s2, eps, o1, o2);
+    const bf16_t n1 = (bf16_t)f2bf(o1), n2 = (bf16_t)f2bf(o2);
+    k_cache[head_off + pos * 128 + lane] = n1;
+    k_cache[head_off + pos * 128 + lane + 64] = n2;
+    reinterpret_cast<bf16_t*>(sm.kns)[lane] = n1;
+    reinterpret_cast<bf16_t*>(sm.kns)[lane + 64] = n2;
+  }
+  if (owns && wave == 1) {
+    v_cache[head_off + pos * 128 + lane] = (bf16_t)k1;
+    v_cache[head_off + pos * 128 + lane + 64] = (bf16_t)k2;
+    reinterpret_cast<bf16_t*>(sm.vns)[lane] = (bf16_t)k1;
+    reinterpret_cast<bf16_t*>(sm.vns)[lane + 64] = (bf16_t)k2;
+  }
+  lds_barrier();
+  // B operand: column c < 4 is query head kvh * 4 + c (dims 32 kk + 8 q4 .. + 7); the other
+  // columns are zero
+  u4v qf[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+    qf[kk] = c < GRP ? reinterpret_cast<const u4v*>(sm.qs[c & (GRP - 1)])[4 * kk + q4]
+                     : u4v{0u, 0u, 0u, 0u};
+  u4v* ks = reinterpret_cast<u4v*>(sm.u.t.ks[wave]);
+  u4v* vs = reinterpret_cast<u4v*>(sm.u.t.vs[wave]);
+  // transposed-read address of V dims 16 dt + 4 (c % 4) .. + 3 of key 16 h2 + 4 q4 + c / 4
+  auto vt_addr = [&](int dt, int h2) -> const void* {
+    const int key = 16 * h2 + 4 * q4 + (c >> 2);
+    const int u = 2 * dt + ((c >> 1) & 1);
+    return reinterpret_cast<const char*>(&vs[key * 16 + (u ^ (key & 15))]) + 8 * (c & 1);
+  };
+  // the new token's unit c of K and V, written over its row by the tile that holds pos
+  const u4v knew = reinterpret_cast<const u4v*>(sm.kns)[c];
+  const u4v vnew = reinterpret_cast<const u4v*>(sm.vns)[c];
+  float m = M_FLOOR, lsum = 0.f;
+  f32x4_t o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int ntiles = kend > start ? (int)((kend - start + 31) / 32) : 0;
+  // stage tile j0 from (kx_, vx_) into this wave's LDS region; the new token's row from LDS
+  auto stage = [&](const u4v (&kx_)[8], const u4v (&vx_)[8], int64_t j0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = q4 + 4 * j;
+      ks[key * 16 + (c ^ (key & 15))] = kx_[j];
+      vs[key * 16 + (c ^ (key & 15))] = vx_[j];
+    }
+    const int64_t pk = pos - j0;                       // LDS keeps a wave's stores in order:
+    if (pk >= 0 && pk < 32 && q4 == 0) {               // this one wins
+      ks[pk * 16 + (c ^ (pk & 15))] = knew;
+      vs[pk * 16 + (c ^ (pk & 15))] = vnew;
+    }
+  };
+  // contract the staged tile at j0 into (m, lsum, o).  The region is this wave's alone and LDS
+  // serves a wave's accesses in order; the fences keep the compiler from moving fragment reads
+  // above the staging stores, or the next staging above these reads.
+  auto contract = [&](int64_t j0) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    f32x4_t sc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int key = 16 * h2 + c;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const u4v kf = ks[key * 16 + ((4 * kk + q4) ^ c)];
+        sc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf),
+                                                        __builtin_bit_cast(bf16x8_t, qf[kk]),
+                                                        sc[h2], 0, 0, 0);
+      }
+    }
+    // lane (c, q4): scores of column c against keys 16 h2 + 4 q4 + r of the tile
+    const int lim = kend - j0 < 32 ? (int)(kend - j0) : 32;
+    float sv[8];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sv[4 * h2 + r] = 16 * h2 + 4 * q4 + r < lim ? sc[h2][r] * scale : NEG_INF;
+    float mx = sv[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
+    mx = fmaxf(mx, lane_xor16(mx));
+    mx = fmaxf(mx, lane_xor32(mx));
+    const float mn = fmaxf(m, mx);
+    const float alpha = __expf(m - mn);
+    m = mn;
+    float p[8], ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { p[e] = __expf(sv[e] - mn); ps += p[e]; }
+    lsum = lsum * alpha + ps;
+    const uint4 pf = make_uint4(pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7]));
+    if (__ballot(alpha != 1.f) != 0) {               // x * 1 == x: skipping changes no bit
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint2 lo = lds_read_tr16(vt_addr(dt, 0));
+      const uint2 hi = lds_read_tr16(vt_addr(dt, 1));
+      const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vf),
+                                                     __builtin_bit_cast(bf16x8_t, pf), o[dt], 0, 0, 0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  };
+  for (int t = wave; t < ntiles; t += DM_NW) {
+    const int64_t j0 = start + 32 * (int64_t)t;
+    stage(kx, vx, j0);
+    DM_LD(kx, vx, j0 + 32 * DM_NW, kend);   // the wave's next tile
+    contract(j0);
+  }
+#undef DM_LD
+  // column totals (the four q4 lanes of a column hold disjoint keys), then the waves' states
+  float l = lsum;
+  l += lane_xor16(l);
+  l += lane_xor32(l);
+  lds_barrier();                          // every wave is done with the staging region
+  if (c < GRP) {
+    if (q4 == 0) { sm.wm[wave][c] = m; sm.wl[wave][c] = l; }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.u.wacc[wave][c][16 * dt + 4 * q4 + r] = o[dt][r];
+  }
+  lds_barrier();
+  if (tid >= GRP * 64) return;            // one head per wave for the combine
+  // as decode_attn_unit: one head per wave, dims d, d + 1 per lane
+  const int h = tid >> 6, d = (tid & 63) * 2;
+  float M = sm.wm[0][h];
+  for (int w = 1; w < DM_NW; ++w) M = fmaxf(M, sm.wm[w][h]);
+  float L = 0.f, A0 = 0.f, A1 = 0.f;
+  for (int w = 0; w < DM_NW; ++w) {
+    const float a = __expf(sm.wm[w][h] - M);
+    L += a * sm.wl[w][h];
+    A0 += a * sm.u.wacc[w][h][d];
+    A1 += a * sm.u.wacc[w][h][d + 1];
+  }
+  const int64_t qrow = b * Hq + kvh * GRP + h;
+  if (splits == 1) {
+    const float inv = 1.0f / L;
+    *reinterpret_cast<uint32_t*>(out + qrow * 128 + d) = pack2(A0 * inv, A1 * inv);
+  } else {
+    const int64_t idx = qrow * splits + split;
+    *reinterpret_cast<float2*>(ws_acc + idx * 128 + d) = make_float2(A0, A1);
+    if ((tid & 63) == 0) *reinterpret_cast<float2*>(ws_ml + idx * 2) = make_float2(M, L);
+  }
+}
+
+static void launch_decode_attn_mfma(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn,
+                                    const bf16_t* kn, const bf16_t* cos_t, const bf16_t* sin_t,
+                                    const int64_t* pos, bf16_t* k_cache, bf16_t* v_cache,
+                                    int64_t B, int Hq, int Hkv, int64_t cap, int64_t splits,
+                                    int64_t chunk, float eps, float* ws_acc, float* ws_ml,
+                                    bf16_t* out, bool rope_row, hipStream_t s) {
+  const dim3 grid((unsigned)splits, (unsigned)Hkv, (unsigned)B), block(DM_NW * 64);
+  const float scale = 1.0f / sqrtf(128.0f);
+  if (rope_row)
+    decode_attn_mfma_kernel<true><<<grid, block, 0, s>>>(qkv, qkv_stride, qn, kn, cos_t, sin_t,
+                                                         pos, k_cache, v_cache, Hq, Hkv, cap,
+                                                         chunk, eps, scale, ws_acc, ws_ml, out);
+  else
+    decode_attn_mfma_kernel<false><<<grid, block, 0, s>>>(qkv, qkv_stride, qn, kn, cos_t, sin_t,
+                                                          pos, k_cache, v_cache, Hq, Hkv, cap,
+                                                          chunk, eps, scale, ws_acc, ws_ml, out);
+}
+
 int64_t block_attn_splits(int64_t cap) { return (cap + BLOCK_CHUNK - 1) / BLOCK_CHUNK; }
 
 // Key splits are only there to fill the chip when few query blocks exist (a tree verification:
