@@ -277,11 +277,12 @@ def decode_ref(qkv, qn, kn, cos, sin, kcache, vcache, pos):
 
 
 # B = 1 runs the VALU unit (shared with the persistent step); B >= 2 the MFMA kernel, whose
-# 32-key tiles make pos = 0 / 31 / 32 and the new key in the last split the edge cases
+# 32-key tiles make pos = 0 / 31 / 32, the new key in the last split, and splits past pos (no
+# keys at all: (2, 4100, 1000) has 13 splits, pos in the fourth) the edge cases
 @pytest.mark.parametrize("B,cap,pos", [(1, 768, 0), (1, 768, 1), (1, 768, 63), (1, 768, 64),
                                        (1, 768, 640), (1, 768, 767), (4, 300, 129),
                                        (32, 2176, 2100), (2, 64, 0), (2, 100, 31), (2, 100, 32),
-                                       (3, 4100, 4099), (8, 600, 257)])
+                                       (3, 4100, 4099), (8, 600, 257), (2, 4100, 1000)])
 def test_decode_attention(ops, B, cap, pos):
     say(f"decode_attention B={B} cap={cap} pos={pos}")
     g = torch.Generator().manual_seed(500 + B + pos)
