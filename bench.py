@@ -3,7 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-b32] [--no-tree] [--no-cpu]
                     [--no-layer]
 
-Workloads:
+Workloads (the benchmark's configurations 2-5; configuration 1 is the CPU parity case):
   value  config 3 -- 36 layers, B=1, prompt 512, up to 256 new tokens: decode tok/s over K timed
          steps (one step = one hipGraph replay of the whole decode step: embed, 36 layers,
          LM head + argmax), after W warm-up steps; inputs resident in HBM.
@@ -399,8 +399,8 @@ def main():
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build is single-GPU (the decode path shards by "
-              "sequence across GPUs with no collective; see DESIGN.md). Run with --gpus 1.",
+        print("bench.py measures one GPU: this build is single-GPU (the decode path would shard "
+              "by sequence, one full weight copy per GPU, with no collective). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
     import torch
