@@ -304,6 +304,26 @@ def test_decode_attention(ops, B, cap, pos):
     assert_ulp(out.cpu(), o_ref, 2, "attention out", abs_floor=p_round_bound(vcache, qkv))
 
 
+@pytest.mark.parametrize("B", [1, 2])
+@pytest.mark.parametrize("pos", [300, -1])
+def test_decode_attention_position_outside_cache_writes_nothing(ops, B, pos):
+    """A device position outside [0, cap) (B = 1: the VALU unit; B = 2: the MFMA kernel) ends
+    every unit before any cache write: both caches come back unchanged."""
+    say(f"decode_attention B={B} pos={pos} (cap 300): no K/V write")
+    g = torch.Generator().manual_seed(77 + B)
+    cap = 300
+    qkv = rnd(g, B, 6144).to(DEV)
+    qn = torch.ones(128, dtype=BF, device=DEV)
+    cos, sin = (t.to(DEV) for t in R.rope_tables(cap))
+    kd = rnd(g, B, 8, cap, 128).to(DEV)
+    vd = rnd(g, B, 8, cap, 128).to(DEV)
+    k0, v0 = kd.clone(), vd.clone()
+    p = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    ops.decode_attention(qkv, qn, qn, cos, sin, p, kd, vd, 32, 8, 1e-6)
+    sync()
+    assert torch.equal(kd, k0) and torch.equal(vd, v0)
+
+
 def test_decode_attention_repeat_is_deterministic(ops):
     say("decode_attention repeat x3 bit-identical (tickets reset)")
     g = torch.Generator().manual_seed(9)
