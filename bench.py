@@ -14,6 +14,9 @@ Workloads (the benchmark's configurations 2-5; configuration 1 is the CPU parity
   layer_kernels  config 2 -- embedding gather, residual-add + RMSNorm, QK-norm + RoPE (+ K/V
          write), SwiGLU at B in {1, 8, 64}: us per launch (1000 launches in one hipGraph) and
          algorithmic GB/s.
+  layer_kernels_large  the same four kernels at row counts that move >= 100 MB per launch
+         (where bandwidth, not launch latency, binds): GB/s, fraction of 8 TB/s, and a device
+         copy of the same bytes as the read+write yardstick.
   step_ms  per-step spread (median, p90, min, max) of the same K steps replayed again with an
          event after each step (the headline timing has no events between steps).
 Weights are seeded random-init N(0, 0.02) generated on the device; prompt ids uniform.
@@ -343,6 +346,103 @@ def layer_kernels(reps=1000):
     return out
 
 
+def _graph_time_us(fn, reps, rounds=5):
+    """Mean µs of one fn() call: fn captured `reps` times into a hipGraph on a side stream,
+    replayed `rounds` times between HIP events on that stream."""
+    import ctypes as C
+
+    import torch
+    from qdecode import _lib
+    st = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        fn()                                             # argument checks outside the capture
+        _lib.call("qd_graph_begin", st.cuda_stream)
+        try:
+            for _ in range(reps):
+                fn()
+        finally:
+            ex = C.c_void_p()
+            rc = _lib.LIB.qd_graph_end(st.cuda_stream, C.byref(ex))
+        if rc != 0:
+            raise _lib.QDError("qd_graph_end", rc)
+        _lib.call("qd_graph_launch", ex, st.cuda_stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(st):
+        e0.record(st)
+        for _ in range(rounds):
+            _lib.call("qd_graph_launch", ex, st.cuda_stream)
+        e1.record(st)
+    torch.cuda.synchronize()
+    _lib.LIB.qd_graph_destroy(ex)
+    return e0.elapsed_time(e1) * 1e3 / (rounds * reps)
+
+
+def layer_kernels_large(reps=20):
+    """The config-2 layer kernels at row counts where bandwidth binds (>= 100 MB per launch;
+    the config's own B <= 64 moves 10 KB - 3.7 MB): embedding gather of 16384 ids, add +
+    RMSNorm of 8192 rows, QK-norm + RoPE + K/V write of 8192 token rows (one sequence at
+    positions 0..8191, i.e. the whole config-2 position range), SwiGLU of 4096 rows.  Bytes
+    are algorithmic (every input read once, every output written once).  `copy_gbs` is a
+    device-to-device copy of the same number of bytes (half read, half written) by the
+    runtime, the read+write stream these kernels compare to; `frac` is of 8 TB/s."""
+    import torch
+    from qdecode import ops
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(11)
+    bf = torch.bfloat16
+    H, I, V, Hq, Hkv = 2560, 9728, 151936, 32, 8
+    out = []
+
+    def record(name, rows, nbytes, fn):
+        us = _graph_time_us(fn, reps)
+        src = torch.empty(nbytes // 4, dtype=torch.int16, device=dev)
+        dst = torch.empty_like(src)
+        cus = _graph_time_us(lambda: dst.copy_(src), reps)
+        del src, dst
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.append({"kernel": name, "rows": rows, "bytes": nbytes, "us_per_launch": round(us, 2),
+                    "achieved_gbs": round(gbs, 1), "frac": round(gbs / 8000.0, 4),
+                    "copy_gbs": round(nbytes / (cus * 1e-6) / 1e9, 1)})
+
+    table = torch.randn((V, H), generator=g, device=dev).to(bf)
+    n = 16384
+    ids = torch.randint(0, V, (n,), generator=g, device=dev)
+    emb = torch.empty((n, H), dtype=bf, device=dev)
+    record("embed_gather", n, 2 * n * H * 2, lambda: ops.embed_gather(ids, table, out=emb))
+    del table, emb
+
+    n = 8192
+    x = torch.randn((n, H), generator=g, device=dev).to(bf)
+    r = torch.randn((n, H), generator=g, device=dev).to(bf)
+    w = torch.ones(H, dtype=bf, device=dev)
+    ro, y = torch.empty_like(r), torch.empty_like(r)
+    record("add_rmsnorm", n, 4 * n * H * 2 + H * 2,
+           lambda: ops.add_rmsnorm(r, w, 1e-6, x=x, res_out=ro, y=y))
+    del x, r, ro, y
+
+    T = 8192
+    qkv = torch.randn((T, (Hq + 2 * Hkv) * 128), generator=g, device=dev).to(bf)
+    cos = torch.randn((T, 128), generator=g, device=dev).to(bf)
+    sin = torch.randn((T, 128), generator=g, device=dev).to(bf)
+    qn = torch.ones(128, dtype=bf, device=dev)
+    q_out = torch.empty((1, T, Hq, 128), dtype=bf, device=dev)
+    kc = torch.zeros((1, Hkv, T, 128), dtype=bf, device=dev)
+    vc = torch.zeros_like(kc)
+    zero = torch.zeros(1, dtype=torch.int64, device=dev)
+    record("qk_norm_rope", T, 2 * T * (Hq + 2 * Hkv) * 128 * 2 + T * 2 * 128 * 2,
+           lambda: ops.qk_norm_rope(qkv, qn, qn, cos, sin, zero, ops.POS_SHARED, q_out, kc, vc,
+                                    1, T, Hq, Hkv, 1e-6))
+    del qkv, q_out, kc, vc
+
+    n = 4096
+    gu = torch.randn((n, 2 * I), generator=g, device=dev).to(bf)
+    act = torch.empty((n, I), dtype=bf, device=dev)
+    record("swiglu", n, 3 * n * I * 2, lambda: ops.swiglu(gu, out=act))
+    return out
+
+
 def cpu_baseline(budget_s=15.0, prompt_len=32):
     """The CPU oracle (torch CPU, oneDNN bf16) on the same 36-layer architecture and
     generator: prefill a short prompt, then time greedy decode steps for ~budget_s."""
@@ -430,7 +530,7 @@ def main():
     log(f"read ceiling over the same weights: {ceil_us:.2f} us/launch, "
         f"{ceil_bytes / (ceil_us * 1e-6) / 1e9:.0f} GB/s (grid {ceil_grid})")
 
-    layer = None
+    layer = layer_large = None
     if not a.no_layer:
         eng.shape = None
         sh = None
@@ -439,6 +539,12 @@ def main():
         for c in layer:
             log(f"config 2 {c['kernel']:>13} B={c['B']:>2}: {c['us_per_launch']:.2f} us/launch, "
                 f"{c['achieved_gbs']:.0f} GB/s")
+        torch.cuda.empty_cache()
+        layer_large = layer_kernels_large()
+        for c in layer_large:
+            log(f"config 2 large {c['kernel']:>13} rows={c['rows']:>5}: {c['us_per_launch']:.2f} "
+                f"us/launch, {c['achieved_gbs']:.0f} GB/s ({c['frac']:.3f} of peak; device copy "
+                f"of the same bytes {c['copy_gbs']:.0f} GB/s)")
         torch.cuda.empty_cache()
 
     b32 = None
@@ -521,6 +627,7 @@ def main():
         "b32": b32,
         "tree": tree,
         "layer_kernels": layer,
+        "layer_kernels_large": layer_large,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -186,7 +186,7 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
     const bf16_t* __restrict__ v_cache, const int64_t* __restrict__ base_ptr,
     const uint64_t* __restrict__ anc, int64_t T, int Hq, int Hkv, int64_t cap, int64_t chunk,
-    float scale, float* ws_acc, float* ws_ml) {
+    float scale, float* ws_acc, float* ws_ml, bf16_t* __restrict__ out) {
   typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
   typedef __attribute__((ext_vector_type(4))) float f32x4_t;
   __shared__ uint4 ks[32 * 16];
@@ -381,6 +381,19 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
     l += lane_xor32(l);
     if (tok[rt] >= T) continue;
     const int64_t idx = ((b * T + tok[rt]) * Hq + kvh * GRP + head) * splits + split;
+    if (splits == 1) {
+      // one key split: the row is complete here.  attn_merge_kernel over one split computes
+      // acc * (1 / l) (its weight exp(m - m) = 1 and sum l are exact), so this store is
+      // bit-identical to the partials + merge it replaces
+      const float inv = 1.0f / l;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const f32x4_t a = o[rt][dt];
+        *reinterpret_cast<uint2*>(out + idx * 128 + 16 * dt + 4 * q4) =
+            make_uint2(pack2(a[0] * inv, a[1] * inv), pack2(a[2] * inv, a[3] * inv));
+      }
+      continue;
+    }
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
       *reinterpret_cast<f32x4_t*>(ws_acc + idx * 128 + 16 * dt + 4 * q4) = o[rt][dt];
@@ -689,7 +702,8 @@ void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_c
   use = (cap + chunk - 1) / chunk;                      // no empty trailing split
   block_attn_mfma_kernel<<<dim3((unsigned)use, (unsigned)Hkv, (unsigned)(B * QB)), dim3(512), 0,
                            s>>>(q, k_cache, v_cache, base, anc, T, Hq, Hkv, cap, chunk,
-                                1.0f / sqrtf(128.0f), ws_acc, ws_ml);
-  attn_merge_kernel<<<dim3((unsigned)(B * T * Hq)), dim3(64), 0, s>>>(ws_acc, ws_ml, (int)use,
-                                                                      out);
+                                1.0f / sqrtf(128.0f), ws_acc, ws_ml, out);
+  if (use > 1)      // one split writes its rows itself
+    attn_merge_kernel<<<dim3((unsigned)(B * T * Hq)), dim3(64), 0, s>>>(ws_acc, ws_ml, (int)use,
+                                                                        out);
 }

@@ -71,7 +71,7 @@ __host__ __device__ inline Layout ll_layout(int L, int64_t splits) {
 }
 
 struct MegaParams {
-  const bf16_t *embed, *final_norm, *w_qkv, *w_o, *w_gu, *w_down, *ln1, *ln2, *q_norm, *k_norm;
+  const bf16_t *embed, *lm_head, *final_norm, *w_qkv, *w_o, *w_gu, *w_down, *ln1, *ln2, *q_norm, *k_norm;
   const bf16_t *cos, *sin;
   bf16_t *k_cache, *v_cache;
   int64_t *tok, *pos;
@@ -508,7 +508,7 @@ __device__ void phase_lm(const MegaParams& p, Smem& sm, int wg, int P, uint32_t*
   uint4 buf[4][5];
 #pragma unroll
   for (int s = 0; s < 4; ++s)
-    if (wave + s * MG_NW < nr) mg_load_row<5>(p.embed, r0 + wave + s * MG_NW, buf[s]);
+    if (wave + s * MG_NW < nr) mg_load_row<5>(p.lm_head, r0 + wave + s * MG_NW, buf[s]);
   const uint4 nw = mg_norm_w<5>(p.final_norm);
   const uint32_t* last = ll + (int64_t)(p.L - 1) * ly.per_layer + ly.out;
   ll_fetch_lds<2>(last, H / 2, p.ctl + 1, reinterpret_cast<uint32_t*>(sm.xs));
@@ -523,7 +523,7 @@ __device__ void phase_lm(const MegaParams& p, Smem& sm, int wg, int P, uint32_t*
       if (k < nr) {
         const float v = rbf(mg_dot<5>(buf[s], sm.xs));   // the reference's logits are bf16
         const int kn = k + 4 * MG_NW;
-        if (kn < nr) mg_load_row<5>(p.embed, r0 + kn, buf[s]);
+        if (kn < nr) mg_load_row<5>(p.lm_head, r0 + kn, buf[s]);
         if (v > bv) { bv = v; bi = (int32_t)(r0 + k); }  // rows ascend per wave: strict >
       }
     }
@@ -647,7 +647,7 @@ int64_t mega_splits(int64_t cap) { return decode_attn_splits(1, HKV, cap); }
 
 hipError_t launch_mega_step(const MegaLaunch& m, hipStream_t s) {
   MegaParams p;
-  p.embed = m.embed; p.final_norm = m.final_norm; p.w_qkv = m.w_qkv; p.w_o = m.w_o;
+  p.embed = m.embed; p.lm_head = m.lm_head; p.final_norm = m.final_norm; p.w_qkv = m.w_qkv; p.w_o = m.w_o;
   p.w_gu = m.w_gu; p.w_down = m.w_down; p.ln1 = m.ln1; p.ln2 = m.ln2; p.q_norm = m.q_norm;
   p.k_norm = m.k_norm; p.cos = m.cos; p.sin = m.sin; p.k_cache = m.k_cache;
   p.v_cache = m.v_cache; p.tok = m.tok; p.pos = m.pos; p.x_out = m.x_out; p.ctl = m.ctl;

@@ -83,6 +83,9 @@ bool weights_ok(const qd_weights* w) {
   return true;
 }
 
+// the LM head's weight: the untied output projection when given, else the tied embedding
+inline const bf16_t* lm_weight(const qd_weights* w) { return w->lm_head ? w->lm_head : w->embed; }
+
 inline int64_t qkv_width(const qd_weights* w) { return (int64_t)(w->n_q_heads + 2 * w->n_kv_heads) * 128; }
 
 }  // namespace
@@ -369,7 +372,7 @@ int qd_decode_step(const qd_weights* w, const qd_decode_state* st, void* stream)
     else
       launch_gemm(st->act, I, B, wd, H, I, st->x, H, st->x, H, EPI_RES, nullptr, nullptr, nullptr, s);
   }
-  return lm_head(st->x, H, w->embed, V, H, B, w->final_norm, w->eps, st->tok, st->pos, nullptr, lw, s);
+  return lm_head(st->x, H, lm_weight(w), V, H, B, w->final_norm, w->eps, st->tok, st->pos, nullptr, lw, s);
 }
 
 // ------------------------------------------------------------------ persistent decode step
@@ -408,7 +411,7 @@ int qd_mega_step(const qd_weights* w, const qd_decode_state* st, void* stream) {
   char* ws = static_cast<char*>(st->workspace);
   const int64_t off = mega_ctl_off(w, st->batch, st->cap);
   MegaLaunch m;
-  m.embed = w->embed; m.final_norm = w->final_norm; m.w_qkv = w->w_qkv; m.w_o = w->w_o;
+  m.embed = w->embed; m.lm_head = lm_weight(w); m.final_norm = w->final_norm; m.w_qkv = w->w_qkv; m.w_o = w->w_o;
   m.w_gu = w->w_gu; m.w_down = w->w_down; m.ln1 = w->ln1; m.ln2 = w->ln2;
   m.q_norm = w->q_norm; m.k_norm = w->k_norm; m.cos = st->cos; m.sin = st->sin;
   m.k_cache = st->k_cache; m.v_cache = st->v_cache; m.tok = st->tok; m.pos = st->pos;
@@ -497,9 +500,9 @@ int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
   }
   if (st->lm_mode == QD_LM_NONE) return launched();
   if (st->lm_mode == QD_LM_LAST)
-    return lm_head(st->x + (T - 1) * H, T * H, w->embed, V, H, B, w->final_norm, w->eps,
+    return lm_head(st->x + (T - 1) * H, T * H, lm_weight(w), V, H, B, w->final_norm, w->eps,
                    st->out_tok, nullptr, nullptr, lw, s);
-  return lm_head(st->x, H, w->embed, V, H, M, w->final_norm, w->eps, st->out_tok, nullptr, nullptr,
+  return lm_head(st->x, H, lm_weight(w), V, H, M, w->final_norm, w->eps, st->out_tok, nullptr, nullptr,
                  lw, s);
 }
 

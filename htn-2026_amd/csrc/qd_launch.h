@@ -79,7 +79,7 @@ int64_t decode_attn_splits(int64_t B, int Hkv, int64_t cap);
 
 // persistent B = 1 decode step (mega.hip)
 struct MegaLaunch {
-  const bf16_t *embed, *final_norm, *w_qkv, *w_o, *w_gu, *w_down, *ln1, *ln2, *q_norm, *k_norm;
+  const bf16_t *embed, *lm_head, *final_norm, *w_qkv, *w_o, *w_gu, *w_down, *ln1, *ln2, *q_norm, *k_norm;
   const bf16_t *cos, *sin;
   bf16_t *k_cache, *v_cache;
   int64_t *tok, *pos;

@@ -41,7 +41,7 @@ TREE_MAX_ROWS = 64        # verification rows B * T: the weight-streaming GEMM r
 class _Shape:
     """Buffers, runners and graphs for one (B, S, N, mode)."""
 
-    def __init__(self, model, stream, B, S, N, tree_T=0, prefill_rows=None):
+    def __init__(self, model, stream, B, S, N, tree_T=0, prefill_rows=None, mega=None):
         self.B, self.S, self.N, self.tree_T = B, S, N, tree_T
         cap = _model.kv_capacity(S, N, extra=tree_T)
         self.kv = _model.KVState(model, B, cap)
@@ -49,13 +49,14 @@ class _Shape:
         self.chunk = _model.prefill_chunk(B, S, prefill_rows or 4096)
         self.prefill = _model.BlockRunner(self.kv, stream, self.chunk, causal=True,
                                            lm_mode=_lib.LM_LAST)
-        self.decode = _model.DecodeRunner(self.kv, stream)
+        self.decode = _model.DecodeRunner(self.kv, stream, mega=mega)
         self.tree = (_model.BlockRunner(self.kv, stream, tree_T, causal=False, lm_mode=_lib.LM_ALL)
                      if tree_T else None)
         self.ids = torch.zeros((B, S), dtype=torch.int64, device=model.device)
         self.ids_host = torch.empty((B, S), dtype=torch.int64, pin_memory=True)
         self.host = torch.empty((max(N, 1), B), dtype=torch.int64, pin_memory=True)
-        self.err_host = torch.zeros((1,), dtype=torch.int32, pin_memory=True)
+        # the persistent step's error word after every step (checked before that step's ids)
+        self.err_host = torch.zeros((max(N, 1),), dtype=torch.int32, pin_memory=True)
         self.events = [torch.cuda.Event() for _ in range(max(N, 1))]
         self.graph_ready = False
 
@@ -100,13 +101,19 @@ class Engine:
         self.tree_mode = TREE_MODE
         self.tree_on = {}                  # (B, S, N) -> the gate's decision
         self.tree_log = {}                 # (B, S, N) -> what the gate measured
+        # Persistent-step tier (engine.py:1038-1045 drops T6 when its error flag fires): None
+        # lets the runner choose (qd_mega_step at B = 1); False after a persistent step
+        # reported an error, so every later shape runs the bit-identical per-launch step.
+        self.mega = None
+        self.mega_errors = []              # (B, S, N, step, error word) of each failure
 
     # -------------------------------------------------------------- state
     def _state(self, B, S, N, tree_T=None):
         """Buffers for (B, S, N) with a tree runner of tree_T nodes (default self.tree_T)."""
         tree_T = self.tree_T if tree_T is None else tree_T
         sh = self.shape
-        if sh is not None and (sh.B, sh.S, sh.N, sh.tree_T) == (B, S, N, tree_T):
+        if sh is not None and (sh.B, sh.S, sh.N, sh.tree_T) == (B, S, N, tree_T) and \
+                not (self.mega is False and sh.decode.mega):
             return sh
         if sh is not None:
             sh.decode.close()
@@ -114,7 +121,8 @@ class Engine:
         gc.collect()
         torch.cuda.empty_cache()
         with torch.cuda.stream(self.stream):
-            sh = _Shape(self.model, self.stream, B, S, N, tree_T, self.prefill_budget_rows)
+            sh = _Shape(self.model, self.stream, B, S, N, tree_T, self.prefill_budget_rows,
+                        mega=self.mega)
         self.stream.synchronize()
         self.shape = sh
         return sh
@@ -145,8 +153,17 @@ class Engine:
             sh = self._state(B, S, N, T)
             key = (B, S, N)
             if T and key not in self.tree_on:
-                self.tree_on[key] = (self.tree_mode == "1" or
-                                     self._decide_tree(sh, ids, min(N, TREE_CHECK_TOKENS)))
+                if self.tree_mode == "1":
+                    self.tree_on[key] = True
+                else:
+                    # the reference disables tree speculation when its gate fails for any
+                    # reason (engine.py:934-936); plain decode then serves this shape
+                    try:
+                        self.tree_on[key] = self._decide_tree(sh, ids, min(N, TREE_CHECK_TOKENS))
+                    except Exception as exc:          # noqa: BLE001  (logged, tier dropped)
+                        self.tree_on[key] = False
+                        self.tree_log[key] = {"on": False, "error": repr(exc)[:200]}
+                        sh = self._state(B, S, N, T)
             if T and self.tree_on[key]:
                 yield from _tree.stream_tree(self, sh, ids, N, _draft.LookaheadDrafter())
             else:
@@ -205,23 +222,34 @@ class Engine:
             with torch.cuda.stream(self.stream):
                 sh.decode.replay()
                 sh.host[t].copy_(sh.kv.tok, non_blocking=True)
-                if err is not None and t in (1, N - 1):   # the persistent step's error word
-                    sh.err_host.copy_(err, non_blocking=True)
+                if err is not None:       # the persistent step's error word, read with its ids
+                    sh.err_host[t:t + 1].copy_(err, non_blocking=True)
                 sh.events[t].record(self.stream)
             sh.events[t - 1].synchronize()
-            if t - 1 == 1:
-                self._check_step(sh)
+            self._check_step(sh, t - 1)
             yield sh.host[t - 1].tolist()
         sh.events[N - 1].synchronize()
-        if N > 1:
-            self._check_step(sh)
+        self._check_step(sh, N - 1)
         yield sh.host[N - 1].tolist()
 
-    @staticmethod
-    def _check_step(sh):
-        if sh.decode.err_word is not None and int(sh.err_host[0]) != 0:
-            raise RuntimeError(f"persistent decode step failed (error word {int(sh.err_host[0])}); "
-                               "QD_MEGA=0 selects the per-launch step")
+    def _check_step(self, sh, t):
+        """Raise before step t's ids are handed out if the persistent step reported an error
+        (a hand-off wait expired or pos fell outside the cache).  The error word stays set from
+        the failing step on, so no id of that step or a later one is yielded.  The runner's
+        workspace is zeroed (epoch, error word and hand-off words start clean) and the engine
+        drops the persistent tier: every later call runs the per-launch step, which is
+        bit-identical to it."""
+        if sh.decode.err_word is None or t == 0:      # step 0 comes from the prefill
+            return
+        code = int(sh.err_host[t])
+        if code == 0:
+            return
+        self.stream.synchronize()
+        sh.decode.reset()
+        self.mega = False
+        self.mega_errors.append((sh.B, sh.S, sh.N, t, code))
+        raise RuntimeError(f"persistent decode step {t} failed (error word {code}); no ids of it "
+                           "were yielded and later calls run the per-launch decode step")
 
     # -------------------------------------------------------------- tree speculation
     def generate_tree(self, input_ids, max_new_tokens, drafter=None, T=64):

@@ -34,7 +34,8 @@ class Weights(C.Structure):
     _fields_ = [("n_layers", i32), ("hidden", i32), ("inter", i32), ("vocab", i32),
                 ("n_q_heads", i32), ("n_kv_heads", i32), ("head_dim", i32), ("eps", f32),
                 ("embed", p), ("final_norm", p), ("w_qkv", p), ("w_o", p), ("w_gu", p),
-                ("w_down", p), ("ln1", p), ("ln2", p), ("q_norm", p), ("k_norm", p)]
+                ("w_down", p), ("ln1", p), ("ln2", p), ("q_norm", p), ("k_norm", p),
+                ("lm_head", p)]
 
 
 class DecodeState(C.Structure):

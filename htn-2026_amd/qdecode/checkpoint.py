@@ -21,11 +21,24 @@ _DTYPES = {"BF16": (np.uint16, torch.bfloat16), "F16": (np.float16, torch.float1
 
 
 def read_config(path):
-    """Model dimensions from config.json (keys as in transformers' Qwen3Config)."""
+    """Model dimensions from config.json, with transformers' Qwen3Config defaults for absent
+    keys (rope_theta 10000, rms_norm_eps 1e-6, tie_word_embeddings False).  RoPE settings come
+    from ``rope_theta`` or from a ``rope_parameters`` dict (transformers >= 5 writes this form);
+    any RoPE scaling other than the default (``rope_scaling`` / ``rope_parameters.rope_type``:
+    linear, dynamic, yarn, ...) is rejected, since the kernels implement plain RoPE."""
     with open(os.path.join(path, "config.json")) as f:
         c = json.load(f)
     rope = c.get("rope_parameters") or {}
-    theta = c.get("rope_theta", rope.get("rope_theta", 1000000.0))
+    scaling = c.get("rope_scaling") or {}
+    theta = c.get("rope_theta", rope.get("rope_theta", 10000.0))
+    for src in (rope, scaling):
+        kind = src.get("rope_type", src.get("type", "default"))
+        if kind not in (None, "default"):
+            raise ValueError(f"rope type {kind!r} is not supported (default RoPE only)")
+    if c.get("use_sliding_window"):
+        # Qwen3 then restricts layers >= max_window_layers to a key window; the kernels attend
+        # over the whole cache
+        raise ValueError("use_sliding_window is not supported (full attention only)")
     heads = c["num_attention_heads"]
     cfg = {
         "hidden_size": int(c["hidden_size"]),
@@ -37,11 +50,8 @@ def read_config(path):
         "vocab_size": int(c["vocab_size"]),
         "rms_norm_eps": float(c.get("rms_norm_eps", 1e-6)),
         "rope_theta": float(theta),
-        "tie_word_embeddings": bool(c.get("tie_word_embeddings", True)),
+        "tie_word_embeddings": bool(c.get("tie_word_embeddings", False)),
     }
-    rope_type = rope.get("rope_type", rope.get("type", "default"))
-    if rope_type not in (None, "default"):
-        raise ValueError(f"rope type {rope_type!r} is not supported (default RoPE only)")
     return cfg
 
 

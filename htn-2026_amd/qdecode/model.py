@@ -77,11 +77,16 @@ class Qwen3Model:
         self.w_down = new(L, H, I)
         self.ln1, self.ln2 = new(L, H), new(L, H)
         self.q_norm, self.k_norm = new(L, D), new(L, D)
+        # the output projection: the embedding itself when tied (engine.py:246-247), else its
+        # own [V, H] tensor (lm_head.weight)
+        self.tied = bool(c.get("tie_word_embeddings", True))
+        self.lm_head = self.embed if self.tied else new(V, H)
         self.qd = _lib.Weights(
             L, H, I, V, Hq, Hkv, D, self.eps, self.embed.data_ptr(), self.final_norm.data_ptr(),
             self.w_qkv.data_ptr(), self.w_o.data_ptr(), self.w_gu.data_ptr(),
             self.w_down.data_ptr(), self.ln1.data_ptr(), self.ln2.data_ptr(),
-            self.q_norm.data_ptr(), self.k_norm.data_ptr())
+            self.q_norm.data_ptr(), self.k_norm.data_ptr(),
+            None if self.tied else self.lm_head.data_ptr())
 
     # -------------------------------------------------------------- where each HF tensor lives
     def slots(self):
@@ -89,6 +94,8 @@ class Qwen3Model:
         D = 128
         nq, nkv = self.Hq * D, self.Hkv * D
         out = [("model.embed_tokens.weight", self.embed), ("model.norm.weight", self.final_norm)]
+        if not self.tied:
+            out.append(("lm_head.weight", self.lm_head))
         for i in range(self.L):
             p = f"model.layers.{i}."
             out += [
@@ -108,18 +115,21 @@ class Qwen3Model:
 
     @classmethod
     def from_checkpoint(cls, path, device="cuda:0"):
+        """Load a local HF checkpoint (engine.py:237-247 without transformers): every tensor of
+        ``slots()`` must be present with its HF shape; an untied checkpoint must hold
+        ``lm_head.weight``."""
         cfg = read_config(path)
-        m = cls(cfg, device)
         st = SafeTensors(path)
+        if not cfg["tie_word_embeddings"] and "lm_head.weight" not in st:
+            raise ValueError("tie_word_embeddings is false but the checkpoint has no lm_head.weight")
+        m = cls(cfg, device)
         for name, dst in m.slots():
+            if name not in st:
+                raise KeyError(f"checkpoint {path} lacks {name}")
             t = st.get(name)
             if tuple(t.shape) != tuple(dst.shape):
                 raise ValueError(f"{name}: checkpoint shape {tuple(t.shape)} != {tuple(dst.shape)}")
             dst.copy_(t.to(BF16), non_blocking=False)
-        if not cfg["tie_word_embeddings"] and "lm_head.weight" in st:
-            lm = st.get("lm_head.weight").to(BF16)
-            if not torch.equal(lm, m.embed.cpu()):
-                raise ValueError("untied lm_head is not supported (the reference ties it)")
         torch.cuda.synchronize(m.device)
         return m
 
@@ -141,9 +151,9 @@ class Qwen3Model:
 
     @property
     def weight_bytes(self):
-        """Algorithmic weight bytes read by one decode step (all projections + tied LM head)."""
+        """Algorithmic weight bytes read by one decode step (all projections + the LM head)."""
         return 2 * (self.w_qkv.numel() + self.w_o.numel() + self.w_gu.numel() + self.w_down.numel()
-                    + self.embed.numel())
+                    + self.lm_head.numel())
 
     @property
     def kv_bytes_per_token(self):
@@ -221,6 +231,13 @@ class DecodeRunner:
         _, err = self.mega_status()
         if err:
             raise RuntimeError(f"persistent decode step failed (error word {err})")
+
+    def reset(self):
+        """Zero the workspace on the runner's stream: the persistent step's epoch, error word
+        and both hand-off copies start clean, as before the first step."""
+        with torch.cuda.stream(self.stream):
+            self.ws.zero_()
+        self.stream.synchronize()
 
     def capture(self):
         """Record one step into a hipGraph (the step has no host inputs: tok/pos are on device)."""

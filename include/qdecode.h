@@ -154,6 +154,8 @@ typedef struct {
   const uint16_t *ln2;        /* [L, hidden] post_attention_layernorm */
   const uint16_t *q_norm;     /* [L, 128] */
   const uint16_t *k_norm;     /* [L, 128] */
+  const uint16_t *lm_head;    /* [vocab, hidden] untied output projection, or NULL: the LM head
+                                 reads embed (tie_word_embeddings, engine.py:246-247) */
 } qd_weights;
 
 /* One greedy decode step for `batch` sequences at the shared device position pos[0]. */

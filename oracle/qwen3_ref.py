@@ -154,12 +154,15 @@ class Qwen3Ref:
         self.theta = cfg["rope_theta"]
         self.p = params
         self.embed = params["model.embed_tokens.weight"]
+        # untied checkpoints carry their own output projection (TF:modeling_qwen3.py:494-495)
+        self.lm_head = params.get("lm_head.weight", self.embed)
 
     @classmethod
-    def from_synth(cls, seed, n_layers):
+    def from_synth(cls, seed, n_layers, tied=True):
         from . import synth
         cfg = dict(synth.QWEN3_4B)
         cfg["num_hidden_layers"] = n_layers
+        cfg["tie_word_embeddings"] = tied
         params = {n: bits_to_bf16(synth.param_bits(seed, n, s))
                   for n, s in synth.param_shapes(cfg).items()}
         return cls(params, cfg)
@@ -203,7 +206,7 @@ class Qwen3Ref:
         if last_only:
             x = x[:, -1:]
         h = rmsnorm(x, self.p["model.norm.weight"], self.eps)
-        logits = linear(h, self.embed)
+        logits = linear(h, self.lm_head)
         return (logits, x) if return_hidden else logits
 
     def decoder_layer(self, i, x):

@@ -45,6 +45,8 @@ def stream_id(name):
     """Tensor id of an HF parameter name (the generator's stream)."""
     if name == "model.embed_tokens.weight":
         return 1
+    if name == "lm_head.weight":                  # untied checkpoints only
+        return 2
     parts = name.split(".")
     layer = int(parts[2])
     kind = {"q_proj": 0, "k_proj": 1, "v_proj": 2, "o_proj": 3,
@@ -157,6 +159,8 @@ def param_shapes(cfg):
     nkv = cfg["num_key_value_heads"] * cfg["head_dim"]
     D = cfg["head_dim"]
     shapes = {"model.embed_tokens.weight": (V, H), "model.norm.weight": (H,)}
+    if not cfg.get("tie_word_embeddings", True):
+        shapes["lm_head.weight"] = (V, H)
     for i in range(cfg["num_hidden_layers"]):
         p = f"model.layers.{i}."
         shapes.update({
@@ -182,40 +186,71 @@ def param_bits(seed, name, shape, std=0.02):
     return tensor_bf16_bits(seed, name, shape, std)
 
 
-def hf_config(cfg):
-    return {
+def hf_config(cfg, rope_form="theta"):
+    """config.json contents.  rope_form "theta" writes ``rope_theta`` (transformers 4.x form),
+    "parameters" only a ``rope_parameters`` dict (the form transformers >= 5 writes)."""
+    c = {
         "architectures": ["Qwen3ForCausalLM"], "model_type": "qwen3",
         "hidden_size": cfg["hidden_size"], "intermediate_size": cfg["intermediate_size"],
         "num_hidden_layers": cfg["num_hidden_layers"],
         "num_attention_heads": cfg["num_attention_heads"],
         "num_key_value_heads": cfg["num_key_value_heads"], "head_dim": cfg["head_dim"],
         "vocab_size": cfg["vocab_size"], "rms_norm_eps": cfg["rms_norm_eps"],
-        "rope_theta": cfg["rope_theta"], "tie_word_embeddings": True,
+        "tie_word_embeddings": bool(cfg.get("tie_word_embeddings", True)),
         "max_position_embeddings": 40960, "hidden_act": "silu", "attention_bias": False,
         "attention_dropout": 0.0, "torch_dtype": "bfloat16", "use_cache": True,
     }
+    if rope_form == "theta":
+        c["rope_theta"] = cfg["rope_theta"]
+    elif rope_form == "parameters":
+        c["rope_parameters"] = {"rope_type": "default", "rope_theta": cfg["rope_theta"]}
+    else:
+        raise ValueError(rope_form)
+    return c
 
 
-def write_checkpoint(path, seed, n_layers, cfg=None, std=0.02):
-    """Write config.json + model.safetensors (bf16, tied embedding: no lm_head tensor)."""
-    cfg = dict(cfg or QWEN3_4B)
-    cfg["num_hidden_layers"] = n_layers
-    os.makedirs(path, exist_ok=True)
-    with open(os.path.join(path, "config.json"), "w") as f:
-        json.dump(hf_config(cfg), f, indent=1)
-    shapes = param_shapes(cfg)
-    names = sorted(shapes)
+def _write_safetensors(path, names, shapes, seed, std, meta):
     header, off = {}, 0
     for n in names:
         nbytes = int(np.prod(shapes[n])) * 2
         header[n] = {"dtype": "BF16", "shape": list(shapes[n]), "data_offsets": [off, off + nbytes]}
         off += nbytes
-    header["__metadata__"] = {"format": "pt", "generator": f"oracle.synth seed={seed} std={std}"}
+    header["__metadata__"] = meta
     hb = json.dumps(header, separators=(",", ":")).encode()
     hb += b" " * (-len(hb) % 8)
-    with open(os.path.join(path, "model.safetensors"), "wb") as f:
+    with open(path, "wb") as f:
         f.write(struct.pack("<Q", len(hb)))
         f.write(hb)
         for n in names:
             f.write(param_bits(seed, n, shapes[n], std).tobytes())
+    return off
+
+
+def write_checkpoint(path, seed, n_layers, cfg=None, std=0.02, shards=1, rope_form="theta",
+                     tied=True):
+    """Write an HF checkpoint directory of the generator's weights: config.json plus
+    model.safetensors (shards == 1) or model-0000i-of-0000n.safetensors files with a
+    model.safetensors.index.json weight map (shards > 1, tensors dealt round-robin in name
+    order so every file holds several kinds).  tied=False adds its own lm_head.weight
+    (generator stream 2) and writes tie_word_embeddings false."""
+    cfg = dict(cfg or QWEN3_4B)
+    cfg["num_hidden_layers"] = n_layers
+    cfg["tie_word_embeddings"] = bool(tied)
+    os.makedirs(path, exist_ok=True)
+    with open(os.path.join(path, "config.json"), "w") as f:
+        json.dump(hf_config(cfg, rope_form), f, indent=1)
+    shapes = param_shapes(cfg)
+    names = sorted(shapes)
+    meta = {"format": "pt", "generator": f"oracle.synth seed={seed} std={std}"}
+    if shards <= 1:
+        _write_safetensors(os.path.join(path, "model.safetensors"), names, shapes, seed, std, meta)
+        return cfg
+    files = [f"model-{i + 1:05d}-of-{shards:05d}.safetensors" for i in range(shards)]
+    groups = [names[i::shards] for i in range(shards)]
+    weight_map, total = {}, 0
+    for fn, group in zip(files, groups):
+        total += _write_safetensors(os.path.join(path, fn), group, shapes, seed, std, meta)
+        weight_map.update({n: fn for n in group})
+    with open(os.path.join(path, "model.safetensors.index.json"), "w") as f:
+        json.dump({"metadata": {"total_size": total}, "weight_map": weight_map}, f, indent=1)
     return cfg

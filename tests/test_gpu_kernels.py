@@ -282,7 +282,9 @@ def decode_ref(qkv, qn, kn, cos, sin, kcache, vcache, pos):
 @pytest.mark.parametrize("B,cap,pos", [(1, 768, 0), (1, 768, 1), (1, 768, 63), (1, 768, 64),
                                        (1, 768, 640), (1, 768, 767), (4, 300, 129),
                                        (32, 2176, 2100), (2, 64, 0), (2, 100, 31), (2, 100, 32),
-                                       (3, 4100, 4099), (8, 600, 257), (2, 4100, 1000)])
+                                       (3, 4100, 4099), (8, 600, 257), (2, 4100, 1000),
+                                       # config-5 context (B = 4, 8192 + a verify's slots)
+                                       (4, 8512, 8447), (1, 8512, 8300)])
 def test_decode_attention(ops, B, cap, pos):
     say(f"decode_attention B={B} cap={cap} pos={pos}")
     g = torch.Generator().manual_seed(500 + B + pos)
@@ -376,6 +378,68 @@ def test_block_attention(ops, mode):
         o = R.attention(q[b:b + 1].transpose(1, 2), kc[b:b + 1], vc[b:b + 1], vis[None, None])
         assert_ulp(out[b].cpu(), o[0].transpose(0, 1), 2, f"block row {b}",
                    abs_floor=p_round_bound(vc))
+
+
+def _tree_masks(T, seed):
+    """Ancestor-or-self masks of a 4-4-2-2 draft tree truncated to T nodes in BFS order (the
+    config-5 tree shape; tests/test_tree_host.py checks the builder)."""
+    from qdecode import tree as tr
+    rng = np.random.default_rng(seed)
+    t = tr.branching_tree(0, T, (4, 4, 2, 2), lambda n: rng.integers(1, 1 << 30, size=n))
+    return t.anc
+
+
+def _block_ref_rows(q, kc, vc, base, anc, T):
+    """Oracle output [B, T, Hq, 128] row by row (visibility from base and masks / causal)."""
+    outs = []
+    cap = kc.shape[2]
+    for b in range(q.shape[0]):
+        vis = torch.zeros((T, cap), dtype=torch.bool)
+        vis[:, :int(base[b])] = True
+        if anc is None:
+            vis[:, int(base[b]):int(base[b]) + T] = torch.tril(torch.ones((T, T), dtype=torch.bool))
+        else:
+            for t in range(T):
+                for jj in range(T):
+                    if (anc[b][t] >> jj) & 1:
+                        vis[t, int(base[b]) + jj] = True
+        o = R.attention(q[b:b + 1].transpose(1, 2), kc[b:b + 1], vc[b:b + 1], vis[None, None])
+        outs.append(o[0].transpose(0, 1))
+    return outs
+
+
+def test_block_attention_config5_verify(ops):
+    """The config-5 verify launch at its real context: B = 4 trees of 64 nodes over 8192 cached
+    keys and more (cap 8512 = 8192 prompt + 256 output + 64 tree slots), different random
+    4-4-2-2 trees per row, bases up to the last legal slot.  B*Hkv = 32 query blocks give the
+    launch's own plan of 8 key splits of 1088 keys each."""
+    B, T, cap = 4, 64, 8512
+    base = torch.tensor([8192, 8193, 8300, cap - T], dtype=torch.int64)
+    say(f"block_attention config 5: B={B} T={T} cap={cap} bases {base.tolist()}")
+    g = torch.Generator().manual_seed(8192)
+    q = rnd(g, B, T, 32, 128, scale=2.0)
+    kc, vc = rnd(g, B, 8, cap, 128), rnd(g, B, 8, cap, 128)
+    anc = [_tree_masks(T, 100 + b) for b in range(B)]
+    anc_t = torch.tensor([[a - (1 << 64) if a >= 1 << 63 else a for a in row] for row in anc])
+    out = ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), base.to(DEV), anc_t.to(DEV))
+    sync()
+    for b, o in enumerate(_block_ref_rows(q, kc, vc, base, anc, T)):
+        assert_ulp(out[b].cpu(), o, 2, f"verify row {b}", abs_floor=p_round_bound(vc))
+
+
+def test_block_attention_causal_chunk_deep(ops):
+    """A causal prefill chunk deep in a config-5 prompt: 1024 tokens per row at base 7168 over a
+    cache of 8512 slots (one key split: 2 x 8 x 16 query blocks fill the chip)."""
+    B, T, cap = 2, 1024, 8512
+    base = torch.tensor([7168, 7168], dtype=torch.int64)
+    say(f"block_attention causal chunk: B={B} T={T} base 7168 cap={cap}")
+    g = torch.Generator().manual_seed(7168)
+    q = rnd(g, B, T, 32, 128, scale=2.0)
+    kc, vc = rnd(g, B, 8, cap, 128), rnd(g, B, 8, cap, 128)
+    out = ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), base.to(DEV), None)
+    sync()
+    for b, o in enumerate(_block_ref_rows(q, kc, vc, base, None, T)):
+        assert_ulp(out[b].cpu(), o, 2, f"chunk row {b}", abs_floor=p_round_bound(vc))
 
 
 def test_kv_compact(ops):

@@ -147,6 +147,37 @@ def test_mega_waits_are_bounded(mods, model4):
     assert 0 <= int(kv.tok.item()) < model4.V
 
 
+def test_engine_persistent_error_is_not_yielded_and_recovers(mods):
+    """Engine.generate reads the persistent step's error word with every step's ids
+    (engine.py:1038-1045 checks the megakernel flag before trusting T6).  The word is set from
+    the host while step 4 runs, so step 5 runs with every wait giving up: generate yields steps
+    0-4 (all equal to a clean run) and raises before step 5's ids.  The workspace is zeroed, the
+    engine drops the persistent tier, and the next call emits the clean run's ids again through
+    the bit-identical per-launch step."""
+    _lib, M = mods
+    from engine import Engine
+    say("Engine.generate with the error word set mid-stream: no post-error ids, recovery")
+    eng = Engine.synthetic(n_layers=4, seed=0)
+    eng.tree_mode = "0"
+    prompt = [list(range(200, 240))]
+    clean = list(eng.generate(prompt, 12))
+    if not eng.shape.decode.mega:
+        pytest.skip("persistent step unsupported on this device")
+    got = []
+    with pytest.raises(RuntimeError, match="persistent decode step 5 failed"):
+        for i, step in enumerate(eng.generate(prompt, 12)):
+            got.append(step)
+            if i == 3:           # step 4 is already enqueued: the word is set behind it
+                with torch.cuda.stream(eng.stream):
+                    eng.shape.decode.err_word.fill_(1)
+    assert got == clean[:5]
+    assert eng.mega is False and eng.mega_errors[-1][3:] == (5, 1)
+    epoch, err = eng.shape.decode.mega_status()
+    assert (epoch, err) == (0, 0)                  # the failed runner's workspace was zeroed
+    again = list(eng.generate(prompt, 12))
+    assert not eng.shape.decode.mega and again == clean
+
+
 def test_engine_mega_matches_per_launch(mods, monkeypatch):
     _lib, M = mods
     from engine import Engine
