@@ -105,7 +105,7 @@ __device__ __forceinline__ void norm_rope_head(const bf16_t* src, const bf16_t* 
                                                float eps, float& o1, float& o2) {
   const int lane = threadIdx.x & 63;
   const float x1 = bf2f(src[lane]), x2 = bf2f(src[lane + 64]);
-  const float r = rstd_of(wave_sum(x1 * x1 + x2 * x2), 128, eps);
+  const float r = rstd_of(wave_sum(sq_pair(x1, x2)), 128, eps);
   const float y1 = norm_elem(x1, r, bf2f(wn[lane])), y2 = norm_elem(x2, r, bf2f(wn[lane + 64]));
   const float c1 = bf2f(cos_row[lane]), c2 = bf2f(cos_row[lane + 64]);
   const float s1 = bf2f(sin_row[lane]), s2 = bf2f(sin_row[lane + 64]);
@@ -130,7 +130,7 @@ __device__ __forceinline__ void group_scores_packed(const uint4 (&qp)[GRP], cons
 __device__ __forceinline__ void norm_rope_vals(float x1, float x2, float w1, float w2, float c1,
                                                float c2, float s1, float s2, float eps, float& o1,
                                                float& o2) {
-  const float r = rstd_of(wave_sum(x1 * x1 + x2 * x2), 128, eps);
+  const float r = rstd_of(wave_sum(sq_pair(x1, x2)), 128, eps);
   const float y1 = norm_elem(x1, r, w1), y2 = norm_elem(x2, r, w2);
   o1 = rbf(rbf(y1 * c1) + rbf(-y2 * s1));
   o2 = rbf(rbf(y2 * c2) + rbf(y1 * s2));

@@ -157,58 +157,101 @@ void launch_add_rmsnorm(const bf16_t* x, const bf16_t* res, const bf16_t* w, bf1
 }
 
 // ------------------------------------------------------------------ q/k RMSNorm + RoPE + KV write
-// One wave per (token row, head in [0, Hq + 2 Hkv)); lane l owns dims l and l + 64, which are
-// exactly the rotate_half partners.  Per-head RMSNorm (q_norm / k_norm weights), then
+// 16 lanes per (token row, head in [0, Hq + 2 Hkv)), 16 heads x 4 rows per workgroup: lane j
+// of a head holds dims 8j .. 8j+7 as one 16-byte load, so a wave moves 1 KiB per access and
+// the rotate_half partner of lane j (dims 64 apart) is lane j ^ 8 of the same DPP row.
+// Per-head RMSNorm (q_norm / k_norm weights), then
 //   o1 = bf16(bf16(y1 c1) + bf16(-y2 s1)),  o2 = bf16(bf16(y2 c2) + bf16(y1 s2))
-// (fused.py:24-81, tree.py:26-69, TF:modeling_qwen3.py:140-170, 252-257).  V heads are
-// copied unnormalised into the cache.  Position of token t of row b:
+// for each (d, d + 64) pair (fused.py:24-81, tree.py:26-69, TF:modeling_qwen3.py:140-170,
+// 252-257).  The 64 sum-of-squares terms sq_pair(x_d, x_{d+64}) are added as a balanced binary
+// tree in index order -- within the lane over its 8 pairs, then across lanes j = 0..7 -- the
+// same tree wave_sum builds over lanes d = 0..63 in the decode attention unit, so the
+// statistics are bit-identical to the decode step's.  V heads are copied unnormalised into
+// the cache.  Position of token t of row b:
 //   POS_T t | POS_SHARED pos[0]+t | POS_ROW pos[b]+t | POS_CHUNK pos[b]+t (= slot)
 //   POS_TREE: RoPE at pos[b] + depth[b*T + t], cache slot pos[b] + t.
-__global__ __launch_bounds__(64) void qk_norm_rope_kernel(
+__device__ __forceinline__ uint32_t row_xor8(uint32_t v) {    // lane ^ 8 within a 16-lane row
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, true);   // row_ror:8
+}
+__device__ __forceinline__ uint4 row_xor8(const uint4 v) {
+  return make_uint4(row_xor8(v.x), row_xor8(v.y), row_xor8(v.z), row_xor8(v.w));
+}
+__device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
+  f[0] = bflo(v.x); f[1] = bfhi(v.x); f[2] = bflo(v.y); f[3] = bfhi(v.y);
+  f[4] = bflo(v.z); f[5] = bfhi(v.z); f[6] = bflo(v.w); f[7] = bfhi(v.w);
+}
+
+constexpr int QKR_ROWS = 4;   // token rows per workgroup: their loads are issued together
+
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const bf16_t* __restrict__ qkv, int64_t qkv_stride, const bf16_t* __restrict__ qn,
     const bf16_t* __restrict__ kn, const bf16_t* __restrict__ cos_t,
     const bf16_t* __restrict__ sin_t, int64_t table_len, const int64_t* __restrict__ pos,
     const int64_t* __restrict__ depth, int mode, bf16_t* __restrict__ q_out,
     bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache, int64_t T, int Hq, int Hkv,
     int64_t cap, float eps) {
-  const int64_t row = blockIdx.x;
-  const int head = blockIdx.y;
-  const int lane = threadIdx.x;
-  const int64_t b = row / T, t = row % T;
-  int64_t rpos, slot;
-  switch (mode) {
-    case POS_T: rpos = slot = t; break;
-    case POS_SHARED: rpos = slot = pos[0] + t; break;
-    case POS_TREE: slot = pos[b] + t; rpos = pos[b] + depth[row]; break;
-    default: rpos = slot = pos[b] + t; break;  // POS_ROW, POS_CHUNK
+  // grid (token blocks of QKR_ROWS, sequence b, head group of 16): no integer division
+  const int head = (int)blockIdx.z * 16 + (threadIdx.x >> 4);
+  if (head >= Hq + 2 * Hkv) return;            // whole 16-lane groups leave together
+  const int64_t b = blockIdx.y;
+  const int64_t t0 = (int64_t)blockIdx.x * QKR_ROWS;
+  const int j = threadIdx.x & 15;
+  const bool vhead = head >= Hq + Hkv, lo = j < 8;
+  uint4 xr[QKR_ROWS];
+#pragma unroll
+  for (int i = 0; i < QKR_ROWS; ++i) {         // every row's 16 bytes in flight at once
+    const int64_t t = t0 + i < T ? t0 + i : T - 1;
+    xr[i] = reinterpret_cast<const uint4*>(qkv + (b * T + t) * qkv_stride + (int64_t)head * 128)[j];
   }
-  const bf16_t* src = qkv + row * qkv_stride + (int64_t)head * 128;
-  if (head >= Hq + Hkv) {  // V: copy into the cache as is
-    if (slot < 0 || slot >= cap) return;
-    const int vh = head - Hq - Hkv;
-    bf16_t* dst = v_cache + ((b * Hkv + vh) * cap + slot) * 128;
-    dst[lane] = src[lane];
-    dst[lane + 64] = src[lane + 64];
-    return;
+  const uint4 w = reinterpret_cast<const uint4*>(head < Hq ? qn : kn)[j];
+#pragma unroll
+  for (int i = 0; i < QKR_ROWS; ++i) {
+    const int64_t t = t0 + i;
+    if (t >= T) break;                         // uniform over the workgroup
+    const int64_t row = b * T + t;
+    int64_t rpos, slot;
+    switch (mode) {
+      case POS_T: rpos = slot = t; break;
+      case POS_SHARED: rpos = slot = pos[0] + t; break;
+      case POS_TREE: slot = pos[b] + t; rpos = pos[b] + depth[row]; break;
+      default: rpos = slot = pos[b] + t; break;  // POS_ROW, POS_CHUNK
+    }
+    const uint4 x = xr[i];
+    if (vhead) {                               // V: copied into the cache as is
+      if (slot >= 0 && slot < cap)
+        reinterpret_cast<uint4*>(v_cache + ((b * Hkv + (head - Hq - Hkv)) * cap + slot) * 128)[j] = x;
+      continue;
+    }
+    if (rpos < 0 || rpos >= table_len) continue;   // per row: the whole group
+    float xs[8], xp[8];
+    unpack8(x, xs);
+    unpack8(row_xor8(x), xp);                  // the partner dims (d +- 64)
+    float sq[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sq[e] = lo ? sq_pair(xs[e], xp[e]) : sq_pair(xp[e], xs[e]);
+    float tot = ((sq[0] + sq[1]) + (sq[2] + sq[3])) + ((sq[4] + sq[5]) + (sq[6] + sq[7]));
+    tot += QD_DPP(tot, 0xB1);                  // lanes j ^ 1
+    tot += QD_DPP(tot, 0x4E);                  // lanes j ^ 2
+    tot += QD_DPP(tot, 0x141);                 // the other 4-lane half of the 8 (row_half_mirror)
+    const float r = rstd_of(tot, 128, eps);
+    const uint4 y = norm8(x, w, r);            // bf16-rounded normed values of my dims
+    float ys[8], yp[8], c[8], sn[8];
+    unpack8(y, ys);
+    unpack8(row_xor8(y), yp);
+    unpack8(reinterpret_cast<const uint4*>(cos_t + rpos * 128)[j], c);
+    unpack8(reinterpret_cast<const uint4*>(sin_t + rpos * 128)[j], sn);
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      o[e] = lo ? rbf(ys[e] * c[e]) + rbf(-yp[e] * sn[e]) : rbf(ys[e] * c[e]) + rbf(yp[e] * sn[e]);
+    const uint4 ov = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]),
+                                pack2(o[6], o[7]));
+    if (head < Hq) {
+      reinterpret_cast<uint4*>(q_out + (row * Hq + head) * 128)[j] = ov;   // q_out [B, T, Hq, 128]
+    } else if (slot >= 0 && slot < cap) {
+      reinterpret_cast<uint4*>(k_cache + ((b * Hkv + (head - Hq)) * cap + slot) * 128)[j] = ov;
+    }
   }
-  if (rpos < 0 || rpos >= table_len) return;
-  const float x1 = bf2f(src[lane]), x2 = bf2f(src[lane + 64]);
-  const float r = rstd_of(wave_sum(x1 * x1 + x2 * x2), 128, eps);
-  const bf16_t* wn = head < Hq ? qn : kn;
-  const float y1 = norm_elem(x1, r, bf2f(wn[lane])), y2 = norm_elem(x2, r, bf2f(wn[lane + 64]));
-  const float c1 = bf2f(cos_t[rpos * 128 + lane]), c2 = bf2f(cos_t[rpos * 128 + lane + 64]);
-  const float s1 = bf2f(sin_t[rpos * 128 + lane]), s2 = bf2f(sin_t[rpos * 128 + lane + 64]);
-  const uint32_t o1 = f2bf(rbf(y1 * c1) + rbf(-y2 * s1));
-  const uint32_t o2 = f2bf(rbf(y2 * c2) + rbf(y1 * s2));
-  bf16_t* dst;
-  if (head < Hq) {
-    dst = q_out + (row * Hq + head) * 128;  // q_out [B, T, Hq, 128]
-  } else {
-    if (slot < 0 || slot >= cap) return;
-    dst = k_cache + ((b * Hkv + (head - Hq)) * cap + slot) * 128;
-  }
-  dst[lane] = (bf16_t)o1;
-  dst[lane + 64] = (bf16_t)o2;
 }
 
 void launch_qk_norm_rope(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn, const bf16_t* kn,
@@ -217,9 +260,11 @@ void launch_qk_norm_rope(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn
                          bf16_t* k_cache, bf16_t* v_cache, int64_t B, int64_t T, int Hq, int Hkv,
                          int64_t cap, float eps, hipStream_t s) {
   if (B * T <= 0) return;
-  qk_norm_rope_kernel<<<dim3((unsigned)(B * T), (unsigned)(Hq + 2 * Hkv)), dim3(64), 0, s>>>(
-      qkv, qkv_stride, qn, kn, cos_t, sin_t, table_len, pos, depth, mode, q_out, k_cache, v_cache,
-      T, Hq, Hkv, cap, eps);
+  const dim3 grid((unsigned)((T + QKR_ROWS - 1) / QKR_ROWS), (unsigned)B,
+                  (unsigned)((Hq + 2 * Hkv + 15) / 16));
+  qk_norm_rope_kernel<<<grid, dim3(256), 0, s>>>(qkv, qkv_stride, qn, kn, cos_t, sin_t, table_len,
+                                                 pos, depth, mode, q_out, k_cache, v_cache, T, Hq,
+                                                 Hkv, cap, eps);
 }
 
 // ------------------------------------------------------------------ SwiGLU

@@ -124,6 +124,7 @@ int qd_qk_norm_rope(const uint16_t* qkv, int64_t qkv_stride, const uint16_t* q_n
                     void* stream) {
   if (batch < 0 || T < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || cap <= 0 || table_len <= 0)
     return QD_EARG;
+  if (batch > 65535) return QD_EARG;           // one grid row per sequence
   if (qkv_stride < (n_q_heads + 2 * n_kv_heads) * 128) return QD_EARG;
   if (mode < QD_POS_T || mode > QD_POS_TREE) return QD_EARG;
   if (batch * T == 0) return QD_OK;
@@ -374,6 +375,7 @@ int qd_decode_step(const qd_weights* w, const qd_decode_state* st, void* stream)
   }
   return lm_head(st->x, H, lm_weight(w), V, H, B, w->final_norm, w->eps, st->tok, st->pos, nullptr, lw, s);
 }
+
 
 // ------------------------------------------------------------------ persistent decode step
 // Workspace: qd_decode_step's region, then (256-byte aligned) the control block {epoch, error}

@@ -87,6 +87,12 @@ __device__ __forceinline__ float dot8(const uint4 a, const uint4 b, float acc) {
   return acc;
 }
 
+// One term of a 128-wide q/k head's sum of squares: dims d (x1) and d + 64 (x2), the
+// rotate_half partners, as one explicit fma.  The decode attention unit (lane d holds both) and
+// qk_norm_rope_kernel (16 lanes per head) add the 64 terms in the same balanced order, so the
+// two compute identical statistics.
+__device__ __forceinline__ float sq_pair(float x1, float x2) { return fmaf(x1, x1, x2 * x2); }
+
 // Qwen3RMSNorm's output element: weight * bf16(x * rstd), rounded to bf16
 __device__ __forceinline__ float norm_elem(float x, float rstd, float w) { return rbf(rbf(x * rstd) * w); }
 

@@ -59,7 +59,7 @@ int qd_add_rmsnorm(const uint16_t *x, const uint16_t *residual, const uint16_t *
 
 /* Per-head q/k RMSNorm + RoPE and the K/V cache write for B*T token rows of a packed qkv
  * [B*T, (Hq + 2 Hkv) * 128].  q_out is [B, T, Hq, 128]; k_cache/v_cache are one layer,
- * [B, Hkv, cap, 128]; cos/sin are [table_len, 128] bf16.
+ * [B, Hkv, cap, 128]; cos/sin are [table_len, 128] bf16; batch <= 65535.
  * Replaces qk_norm_rope_cache (engine/kernels/fused.py:84-98) and tree_qk (tree.py:198-204). */
 int qd_qk_norm_rope(const uint16_t *qkv, int64_t qkv_stride, const uint16_t *q_norm_w,
                     const uint16_t *k_norm_w, const uint16_t *cos, const uint16_t *sin,

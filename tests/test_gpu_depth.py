@@ -1,0 +1,111 @@
+"""GPU end-to-end parity at the benchmark configs' real depth and context: the full 36-layer
+seeded model (seed 1) through Engine.generate / generate_tree, against the CPU oracle.
+
+  config 3  B=1, S=512, 32 tokens (the persistent step): ids against the stored oracle greedy
+            run (tests/golden/depth.json) and, teacher-forced on the engine's own ids, one
+            36-layer oracle forward on this host under the north-star margin rule
+  config 4  B=32, S=2048, 4 tokens (MFMA projections, MFMA decode attention over 36 x 2048
+            cached keys): rows 0 and 31 against the stored oracle run, row 0 teacher-forced
+  config 5  B=4, S=8192, tree verification with random 4-4-2-2 drafts (64-node trees) and
+            plain decode at the same context: rows 0 and 1 against the stored oracle run
+
+The stored runs come from tests/golden/make_depth_golden.py (the same oracle, prompts from
+synth.prompt_ids).  Token rule against a stored run (helpers.fixture_rule): identical ids, the
+first difference allowed only at an oracle near tie (top-2 gap within 2 bf16 ulp) where the
+engine picked the oracle's second choice."""
+
+import json
+import os
+import time
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import GOLDEN, ORACLE_TIE, ensure_oracle_built, fixture_rule, margin_rule
+from oracle import qwen3_ref as R
+from oracle import synth
+
+pytestmark = pytest.mark.gpu
+DEPTH = json.load(open(os.path.join(GOLDEN, "depth.json")))
+
+
+def say(msg):
+    print(f"\n[case] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def eng36():
+    from engine import Engine
+    say("Engine.synthetic(36 layers, seed 1)")
+    e = Engine.synthetic(n_layers=36, seed=1)
+    e.tree_mode = "0"            # plain decode unless a test asks for trees
+    return e
+
+
+@pytest.fixture(scope="module")
+def ref36():
+    ensure_oracle_built()
+    torch.set_num_threads(min(16, len(os.sched_getaffinity(0))))
+    t0 = time.time()
+    ref = R.Qwen3Ref.from_synth(1, 36)
+    print(f"[oracle] 36-layer weights in {time.time() - t0:.1f} s", flush=True)
+    return ref
+
+
+def _prompts(name):
+    c = DEPTH[name]
+    return synth.prompt_ids(c["seed"], c["B"], c["S"]), c
+
+
+def _teacher(ref, prompt_row, toks_row, what):
+    t0 = time.time()
+    tl = ref.teacher_logits(prompt_row[None], toks_row[None])
+    print(f"[oracle] teacher-forced {what}: {prompt_row.shape[0] + toks_row.shape[0] - 1} "
+          f"tokens in {time.time() - t0:.1f} s", flush=True)
+    return tl
+
+
+def test_config3_end_to_end(eng36, ref36):
+    prompt, c = _prompts("config3")
+    say(f"config 3: 36 layers, B=1, S={c['S']}, N={c['N']}")
+    toks = np.array(list(eng36.generate(prompt.tolist(), c["N"]))).T      # [1, N]
+    from qdecode import model as M
+    assert eng36.shape.decode.mega == M.mega_default(eng36.model, 1)   # the benchmark's tier
+    print(f"persistent step: {eng36.shape.decode.mega}; ids {toks[0].tolist()}", flush=True)
+    fixture_rule(toks[0], c["rows"][0])
+    tl = _teacher(ref36, prompt[0], toks[0], "config 3")
+    assert margin_rule(toks, tl, margin=ORACLE_TIE, what="config 3, 36 layers") == []
+
+
+def test_config4_end_to_end(eng36, ref36):
+    prompt, c = _prompts("config4")
+    say(f"config 4: 36 layers, B={c['B']}, S={c['S']}, N={c['N']}")
+    toks = np.array(list(eng36.generate(prompt.tolist(), c["N"]))).T      # [B, N]
+    assert toks.shape == (c["B"], c["N"])
+    for rec in c["rows"]:
+        print(f"row {rec['row']}: {toks[rec['row']].tolist()}", flush=True)
+        fixture_rule(toks[rec["row"]], rec)
+    tl = _teacher(ref36, prompt[0], toks[0], "config 4 row 0")
+    assert margin_rule(toks[:1], tl, margin=ORACLE_TIE, what="config 4 row 0") == []
+
+
+def test_config5_tree_and_plain_at_8192(eng36):
+    """Exact tree verification at the config-5 context: the emitted ids of a random-draft tree
+    run equal the stored oracle greedy ids, and so do the plain decode's (B=4 MFMA decode
+    attention over 8192+ keys)."""
+    from qdecode import tree as tr
+    prompt, c = _prompts("config5")
+    say(f"config 5: 36 layers, B={c['B']}, S={c['S']}, N={c['N']}, 64-node random trees")
+    got = np.array(list(eng36.generate_tree(prompt.tolist(), c["N"], tr.random_tree_drafter(5),
+                                            T=64))).T
+    stats = eng36.tree_stats
+    print(f"tree passes {stats['passes']} accepted {stats['accepted']}", flush=True)
+    assert got.shape == (c["B"], c["N"])
+    for rec in c["rows"]:
+        print(f"tree row {rec['row']}: {got[rec['row']].tolist()}", flush=True)
+        fixture_rule(got[rec["row"]], rec)
+    plain = np.array(list(eng36.generate(prompt.tolist(), c["N"]))).T
+    for rec in c["rows"]:
+        print(f"plain row {rec['row']}: {plain[rec['row']].tolist()}", flush=True)
+        fixture_rule(plain[rec["row"]], rec)

@@ -276,6 +276,30 @@ def decode_ref(qkv, qn, kn, cos, sin, kcache, vcache, pos):
     return o[:, :, 0], kc, vc
 
 
+@pytest.mark.parametrize("B", [1, 4])
+def test_qk_norm_rope_matches_decode_unit_bitwise(ops, B):
+    """The standalone q/k norm + RoPE kernel (prefill chunks, tree verification: 16 lanes per
+    head) and the decode attention unit's prologue (one lane per dim pair; B = 1 the VALU unit
+    shared with the persistent step, B = 4 the MFMA kernel) add the head's sum of squares in
+    the same order: the K / V rows they write to the cache are bit-identical."""
+    say(f"qk_norm_rope vs decode attention prologue, B={B}: identical K/V writes")
+    g = torch.Generator().manual_seed(4242 + B)
+    cap, pos = 600, 517
+    qkv = rnd(g, B, 6144, scale=3.0).to(DEV)
+    qn, kn = (rnd(g, 128, scale=0.2) + 1).to(DEV), (rnd(g, 128, scale=0.2) + 1).to(DEV)
+    cos, sin = (t.to(DEV) for t in R.rope_tables(cap))
+    p = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    k1 = torch.zeros((B, 8, cap, 128), dtype=BF, device=DEV)
+    v1 = torch.zeros_like(k1)
+    ops.decode_attention(qkv, qn, kn, cos, sin, p, k1, v1, 32, 8, 1e-6)
+    k2, v2 = torch.zeros_like(k1), torch.zeros_like(k1)
+    q_out = torch.empty((B, 1, 32, 128), dtype=BF, device=DEV)
+    ops.qk_norm_rope(qkv, qn, kn, cos, sin, p, ops.POS_SHARED, q_out, k2, v2, B, 1, 32, 8, 1e-6)
+    sync()
+    assert torch.equal(k1.view(torch.int16), k2.view(torch.int16))
+    assert torch.equal(v1.view(torch.int16), v2.view(torch.int16))
+
+
 # B = 1 runs the VALU unit (shared with the persistent step); B >= 2 the MFMA kernel, whose
 # 32-key tiles make pos = 0 / 31 / 32, the new key in the last split, and splits past pos (no
 # keys at all: (2, 4100, 1000) has 13 splits, pos in the fourth) the edge cases
