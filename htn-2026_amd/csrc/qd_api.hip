@@ -4,6 +4,8 @@
 
 #include <string.h>
 
+#include <mutex>
+
 #include "qd_launch.h"
 
 namespace {
@@ -374,6 +376,61 @@ int qd_decode_step(const qd_weights* w, const qd_decode_state* st, void* stream)
       launch_gemm(st->act, I, B, wd, H, I, st->x, H, st->x, H, EPI_RES, nullptr, nullptr, nullptr, s);
   }
   return lm_head(st->x, H, lm_weight(w), V, H, B, w->final_norm, w->eps, st->tok, st->pos, nullptr, lw, s);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ decode step, no allocation
+// The split partials of qd_decode_step_noalloc.  In host code `scratch` names a host-side
+// stand-in, not device memory: only the address hipGetSymbolAddress returns (per device) may
+// reach a kernel or a copy.  qd_decode_step's workspace is written before it is read within a
+// step, so the array needs no clearing between calls.
+static __device__ __align__(256) unsigned char scratch[QD_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};   // device address of `scratch` per device, once resolved
+
+// Device address of `scratch` on the current device, resolved once per device (the module's
+// copy of the array is per device, at its own address).
+int scratch_on_current_device(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return qd_err(e);
+  if (dev < 0 || dev >= kMaxDevices) return QD_EARG;
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return qd_err(e);
+    if (sdev != dev) return QD_EARG;   // the array resolved here would belong to another GPU
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return e != hipSuccess ? qd_err(e) : QD_ESTATE;
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return QD_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int qd_decode_step_noalloc(const qd_weights* w, const qd_decode_state* st, void* stream) {
+  if (!weights_ok(w) || !st || st->batch <= 0 || st->cap <= 0) return QD_EARG;
+  const int64_t need = qd_decode_workspace_bytes(w, st->batch, st->cap);
+  if (need <= 0) return QD_EARG;
+  if (need > (int64_t)QD_NOALLOC_SCRATCH_BYTES) return QD_ESCRATCH;
+  void* ptr = nullptr;
+  const int rc = scratch_on_current_device(S(stream), &ptr);
+  if (rc != QD_OK) return rc;
+  qd_decode_state s2 = *st;
+  s2.workspace = ptr;
+  s2.workspace_bytes = QD_NOALLOC_SCRATCH_BYTES;
+  return qd_decode_step(w, &s2, stream);
 }
 
 

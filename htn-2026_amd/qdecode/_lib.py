@@ -11,7 +11,8 @@ import os
 HERE = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.environ.get("QDECODE_LIB", os.path.join(HERE, "libqdecode.so"))
 
-QD_EARG, QD_EWS, QD_ESTATE = -1, -2, -3
+QD_EARG, QD_EWS, QD_ESTATE, QD_ESCRATCH = -1, -2, -3, -4
+QD_NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024
 EPI_NONE, EPI_RES, EPI_SWIGLU = 0, 1, 2
 POS_T, POS_SHARED, POS_ROW, POS_TREE = 0, 1, 2, 3
 LM_ALL, LM_LAST, LM_NONE = 0, 1, 2
@@ -24,7 +25,8 @@ class QDError(RuntimeError):
 
     def __init__(self, fn, rc):
         names = {QD_EARG: "invalid argument", QD_EWS: "workspace too small",
-                 QD_ESTATE: "invalid state"}
+                 QD_ESTATE: "invalid state",
+                 QD_ESCRATCH: "step needs more than the library's static scratch"}
         super().__init__(f"{fn} failed: {names.get(rc, f'hipError {rc}')} (rc={rc})")
         self.rc = rc
 
@@ -75,6 +77,7 @@ SIGNATURES = {
     "qd_read_probe": ([p, i64, i32, p, p], i32),
     "qd_decode_workspace_bytes": ([C.POINTER(Weights), i64, i64], i64),
     "qd_decode_step": ([C.POINTER(Weights), C.POINTER(DecodeState), p], i32),
+    "qd_decode_step_noalloc": ([C.POINTER(Weights), C.POINTER(DecodeState), p], i32),
     "qd_mega_supported": ([C.POINTER(Weights), i64], i32),
     "qd_mega_workspace_bytes": ([C.POINTER(Weights), i64, i64], i64),
     "qd_mega_ctl_offset": ([C.POINTER(Weights), i64, i64], i64),

@@ -181,6 +181,21 @@ typedef struct {
 int64_t qd_decode_workspace_bytes(const qd_weights *w, int64_t batch, int64_t cap);
 int qd_decode_step(const qd_weights *w, const qd_decode_state *st, void *stream);
 
+/* qd_decode_step without a caller workspace.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The step's split partials live in a file-scope device array
+ * of QD_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends); st->workspace and
+ * st->workspace_bytes are ignored.  Same kernels and results as qd_decode_step (bit-identical).
+ * Returns QD_ESCRATCH, before touching the device, when qd_decode_workspace_bytes(w, batch, cap)
+ * exceeds the array (at Qwen3-4B's shape batch 32 fits up to cap 106496, batch 64 up to 40960).
+ * The stream must belong to the current device.  Every call on one GPU shares that GPU's
+ * array, whose contents the next call overwrites: calls that overlap on one GPU
+ * (different streams, or host threads) race and must be serialised by the caller.  Allocates
+ * nothing (no hipMalloc / hipFree, no allocating library call). */
+#define QD_ESCRATCH (-4)
+#define QD_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int qd_decode_step_noalloc(const qd_weights *w, const qd_decode_state *st, void *stream);
+
 /* The same step (batch == 1) as ONE persistent launch of one workgroup per CU that hands
  * activations between phases through hand-off words in the workspace instead of launch
  * boundaries.
