@@ -148,6 +148,62 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
   }
 }
 
+// Split-K partials + residual add + RMSNorm (the batched decode step's o / down projections
+// end here): acc = sum of part[s][row] in split order (fp32), r' = bf16(res + bf16(acc))
+// written back to res -- the residual epilogue's rounding points (gemv.py:50-51) -- and
+// y = bf16(bf16(r' * rstd) * w).  One workgroup per row, hidden <= 8192.
+__global__ __launch_bounds__(256) void part_add_rmsnorm_kernel(
+    const float* __restrict__ part, int S, int64_t rows, bf16_t* res, const bf16_t* __restrict__ w,
+    bf16_t* __restrict__ y, int64_t hidden, float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int64_t nch = hidden / 8;
+  uint4* rr = reinterpret_cast<uint4*>(res + row * hidden);
+  const uint4* wr = reinterpret_cast<const uint4*>(w);
+  uint4* yr = reinterpret_cast<uint4*>(y + row * hidden);
+  float ss = 0.f;
+  uint4 rv[AR_MAXC], gv[AR_MAXC];
+#pragma unroll
+  for (int j = 0; j < AR_MAXC; ++j) {
+    const int64_t c = threadIdx.x + 256 * j;
+    if (c < nch) {
+      const float4* p = reinterpret_cast<const float4*>(part + row * hidden) + 2 * c;
+      float4 a = p[0], b = p[1];
+      for (int s = 1; s < S; ++s) {
+        const float4* ps = reinterpret_cast<const float4*>(part + ((int64_t)s * rows + row) * hidden) + 2 * c;
+        const float4 a2 = ps[0], b2 = ps[1];
+        a.x += a2.x; a.y += a2.y; a.z += a2.z; a.w += a2.w;
+        b.x += b2.x; b.y += b2.y; b.z += b2.z; b.w += b2.w;
+      }
+      const uint4 r = rr[c];
+      uint4 o;
+      o.x = pack2(bflo(r.x) + rbf(a.x), bfhi(r.x) + rbf(a.y));
+      o.y = pack2(bflo(r.y) + rbf(a.z), bfhi(r.y) + rbf(a.w));
+      o.z = pack2(bflo(r.z) + rbf(b.x), bfhi(r.z) + rbf(b.y));
+      o.w = pack2(bflo(r.w) + rbf(b.z), bfhi(r.w) + rbf(b.w));
+      rv[j] = o;
+      gv[j] = wr[c];
+      ss += sumsq8(o);
+    }
+  }
+  const float rstd = rstd_of(block_sum256(ss, red), (int)hidden, eps);
+#pragma unroll
+  for (int j = 0; j < AR_MAXC; ++j) {
+    const int64_t c = threadIdx.x + 256 * j;
+    if (c < nch) {
+      yr[c] = norm8(rv[j], gv[j], rstd);
+      rr[c] = rv[j];                             // each thread writes back the chunks it read
+    }
+  }
+}
+
+void launch_part_add_rmsnorm(const float* part, int S, int64_t rows, bf16_t* res, const bf16_t* w,
+                             bf16_t* y, int64_t hidden, float eps, hipStream_t s) {
+  if (rows <= 0) return;
+  part_add_rmsnorm_kernel<<<dim3((unsigned)rows), dim3(256), 0, s>>>(part, S, rows, res, w, y,
+                                                                      hidden, eps);
+}
+
 void launch_add_rmsnorm(const bf16_t* x, const bf16_t* res, const bf16_t* w, bf16_t* res_out,
                         bf16_t* y, int64_t rows, int64_t hidden, int64_t in_stride,
                         int64_t y_stride, float eps, hipStream_t s) {

@@ -593,6 +593,11 @@ static int64_t gemm_mt(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, 
       return stream_mt<4, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, P, s);
     }
   }
+  if constexpr (EPI != EPI_ARGMAX) {
+    // 3..32 rows: the skinny kernel (one workgroup per CU, waves split K), unsplit here
+    if (M <= 32 && launch_gemm_skinny(x, xs, M, w, N, K, EPI, 1, out, os, res, rs, nullptr, s))
+      return 0;
+  }
   if (M <= 64 && K % 512 == 0) {
     if (M <= 16) gemm_lds_go<1, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);
     else gemm_lds_go<2, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, s);

@@ -74,6 +74,15 @@ int lm_head(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t V, int64
   return launched();
 }
 
+// LM head + argmax over `rows` already-normalised rows xn [rows, K] (the MFMA path)
+int lm_head_normed(const bf16_t* xn, const bf16_t* w, int64_t V, int64_t K, int64_t rows,
+                   int64_t* tok, int64_t* pos_inc, const LmWs& l, hipStream_t s) {
+  const int64_t parts = launch_gemm(xn, K, rows, w, V, K, nullptr, 0, nullptr, 0, EPI_ARGMAX,
+                                    l.val, l.idx, nullptr, s);
+  launch_argmax_reduce(l.val, l.idx, parts, rows, tok, pos_inc, s);
+  return launched();
+}
+
 bool weights_ok(const qd_weights* w) {
   if (!w || !w->embed || !w->final_norm || !w->w_qkv || !w->w_o || !w->w_gu || !w->w_down ||
       !w->ln1 || !w->ln2 || !w->q_norm || !w->k_norm)
@@ -83,6 +92,39 @@ bool weights_ok(const qd_weights* w) {
     return false;
   if (w->hidden % 128 || w->inter % 128 || (w->n_q_heads * 128) % 128) return false;
   return true;
+}
+
+// Batched decode (3..32 rows) on the skinny kernel: K splits of the o and down projections
+// (their partials are summed by the following residual-add + RMSNorm launch); qkv and gate/up
+// run unsplit.  Measured per projection at 32 rows on MI355X.
+#ifndef QD_SK_SPLIT_O
+#define QD_SK_SPLIT_O 2
+#endif
+#ifndef QD_SK_SPLIT_DOWN
+#define QD_SK_SPLIT_DOWN 4
+#endif
+constexpr int SK_SPLIT_O = QD_SK_SPLIT_O, SK_SPLIT_DOWN = QD_SK_SPLIT_DOWN;
+
+// Whether a B-row step runs the skinny path: shapes only (the workspace size depends on it), and
+// with a state, also the alignment of the step's own buffers (checked before anything launches)
+bool skinny_step_ok(const qd_weights* w, int64_t B, const qd_decode_state* st = nullptr) {
+  if (B < 3 || B > 32) return false;
+  const int64_t H = w->hidden, I = w->inter, QD = (int64_t)w->n_q_heads * 128;
+  const int64_t NQKV = (int64_t)(w->n_q_heads + 2 * w->n_kv_heads) * 128;
+  const void* a = reinterpret_cast<const void*>(256);    // workspace regions: 256-aligned
+  const void* attn = st ? st->attn : a;
+  const void* act = st ? st->act : a;
+  return skinny_ok(B, NQKV, H, EPI_NONE, 1, a, H, st ? w->w_qkv : a, NQKV) &&
+         skinny_ok(B, H, QD, EPI_NONE, SK_SPLIT_O, attn, QD, st ? w->w_o : a, H) &&
+         skinny_ok(B, I, H, EPI_SWIGLU, 1, a, H, st ? w->w_gu : a, I) &&
+         skinny_ok(B, H, I, EPI_NONE, SK_SPLIT_DOWN, act, I, st ? w->w_down : a, H) &&
+         (!st || (reinterpret_cast<uintptr_t>(st->qkv) % 8 == 0 &&
+                  reinterpret_cast<uintptr_t>(st->act) % 8 == 0));
+}
+
+int64_t skinny_step_part_floats(const qd_weights* w, int64_t B) {
+  const int S = SK_SPLIT_O > SK_SPLIT_DOWN ? SK_SPLIT_O : SK_SPLIT_DOWN;
+  return skinny_part_floats(B, w->hidden, S);
 }
 
 // the LM head's weight: the untied output projection when given, else the tied embedding
@@ -315,6 +357,7 @@ int64_t qd_decode_workspace_bytes(const qd_weights* w, int64_t batch, int64_t ca
   carve_lm(c, batch, w->vocab, w->hidden);
   c.take<bf16_t>(batch * (int64_t)w->hidden);  // normalised activations (MFMA path)
   c.take<bf16_t>(256);                         // this step's RoPE row
+  if (skinny_step_ok(w, batch)) c.take<float>(skinny_step_part_floats(w, batch));
   return c.off;
 }
 
@@ -338,6 +381,32 @@ int qd_decode_step(const qd_weights* w, const qd_decode_state* st, void* stream)
   const bool vec_h = gemv_supported(B, H), vec_q = gemv_supported(B, QD), vec_i = gemv_supported(B, I);
 
   launch_embed_rope(st->tok, w->embed, st->x, B, V, H, H, st->cos, st->sin, st->pos, cap, rope_row, s);
+  if (skinny_step_ok(w, B)) {
+    if (!skinny_step_ok(w, B, st)) return QD_EARG;       // misaligned step buffers
+    // 3..32 rows: skinny GEMMs; the o / down K-split partials are folded into the residual by
+    // the next RMSNorm launch (r' = bf16(x + bf16(sum of partials)), the EPI_RES rounding)
+    float* part = c.take<float>(skinny_step_part_floats(w, B));
+    launch_add_rmsnorm(nullptr, st->x, w->ln1, nullptr, xn, B, H, H, H, w->eps, s);
+    for (int64_t l = 0; l < w->n_layers; ++l) {
+      if (l > 0)
+        launch_part_add_rmsnorm(part, SK_SPLIT_DOWN, B, st->x, w->ln1 + l * H, xn, H, w->eps, s);
+      launch_gemm_skinny(xn, H, B, w->w_qkv + l * NQKV * H, NQKV, H, EPI_NONE, 1, st->qkv, NQKV,
+                         nullptr, 0, nullptr, s);
+      launch_decode_attn(st->qkv, NQKV, w->q_norm + l * 128, w->k_norm + l * 128, rope_row,
+                         rope_row + 128, st->pos, st->k_cache + l * layer_kv,
+                         st->v_cache + l * layer_kv, B, Hq, Hkv, cap, splits, w->eps, aw.acc,
+                         aw.ml, st->attn, true, s);
+      launch_gemm_skinny(st->attn, QD, B, w->w_o + l * H * QD, H, QD, EPI_NONE, SK_SPLIT_O,
+                         nullptr, 0, nullptr, 0, part, s);
+      launch_part_add_rmsnorm(part, SK_SPLIT_O, B, st->x, w->ln2 + l * H, xn, H, w->eps, s);
+      launch_gemm_skinny(xn, H, B, w->w_gu + l * 2 * I * H, I, H, EPI_SWIGLU, 1, st->act, I,
+                         nullptr, 0, nullptr, s);
+      launch_gemm_skinny(st->act, I, B, w->w_down + l * H * I, H, I, EPI_NONE, SK_SPLIT_DOWN,
+                         nullptr, 0, nullptr, 0, part, s);
+    }
+    launch_part_add_rmsnorm(part, SK_SPLIT_DOWN, B, st->x, w->final_norm, lw.xn, H, w->eps, s);
+    return lm_head_normed(lw.xn, lm_weight(w), V, H, B, st->tok, st->pos, lw, s);
+  }
   for (int64_t l = 0; l < w->n_layers; ++l) {
     const bf16_t* wqkv = w->w_qkv + l * NQKV * H;
     const bf16_t* wo = w->w_o + l * H * QD;

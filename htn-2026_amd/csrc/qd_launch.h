@@ -21,6 +21,9 @@ void launch_embed_rope(const int64_t* ids, const bf16_t* table, bf16_t* out, int
 void launch_add_rmsnorm(const bf16_t* x, const bf16_t* res, const bf16_t* w, bf16_t* res_out,
                         bf16_t* y, int64_t rows, int64_t hidden, int64_t in_stride, int64_t y_stride,
                         float eps, hipStream_t s);
+// split-K partials [S][rows][hidden] fp32 + residual (in/out) + RMSNorm
+void launch_part_add_rmsnorm(const float* part, int S, int64_t rows, bf16_t* res, const bf16_t* w,
+                             bf16_t* y, int64_t hidden, float eps, hipStream_t s);
 void launch_qk_norm_rope(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn, const bf16_t* kn,
                          const bf16_t* cos_t, const bf16_t* sin_t, int64_t table_len,
                          const int64_t* pos, const int64_t* depth, int mode, bf16_t* q_out,
@@ -56,6 +59,15 @@ int64_t launch_gemm(const bf16_t* x, int64_t x_stride, int64_t M, const bf16_t* 
                     int64_t K, bf16_t* out, int64_t out_stride, const bf16_t* res,
                     int64_t res_stride, int epi, float* pval, int32_t* pidx, float* logits,
                     hipStream_t s, float* part = nullptr, int64_t part_floats = 0);
+// gemm_skinny.hip (batched decode, M <= 32: one workgroup per CU, waves split K).  part == NULL:
+// the epilogue writes out (S == 1); else fp32 split-K partials part[S][M][N] for the caller to
+// sum.  Returns false (nothing launched) for an unsupported shape or a missing destination.
+bool skinny_ok(int64_t M, int64_t N, int64_t K, int epi, int S, const void* x, int64_t xs,
+               const void* w, int64_t os);
+int64_t skinny_part_floats(int64_t M, int64_t N, int S);
+bool launch_gemm_skinny(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
+                        int64_t K, int epi, int S, bf16_t* out, int64_t os, const bf16_t* res,
+                        int64_t rs, float* part, hipStream_t s);
 // gemm_tile.hip (LDS-tiled MFMA GEMM for M > 64)
 bool gemm_tile_ok(int64_t M, int64_t N, int64_t K, int epi, const void* x, int64_t x_stride,
                   const void* w, const void* out, int64_t out_stride, const void* res,

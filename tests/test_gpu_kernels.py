@@ -135,11 +135,12 @@ def exact_linear(x, w):
 SHAPES = {"qkv": (6144, 2560), "o": (2560, 4096), "gu": (9728, 2560), "down": (2560, 9728)}
 
 
-# 1..64 rows: vector GEMV / weight-streaming MFMA kernels; 100, 256, 600 rows: the LDS-tiled
+# 1..2 rows: vector GEMV; 3..32: the skinny kernel (one workgroup per CU; 20 rows: a ragged
+# second activation tile); 64: the LDS-staged MFMA kernel; 100, 256, 600 rows: the LDS-tiled
 # kernel (128-row tiles with a ragged last tile; K split over workgroups with the fp32 partials
 # summed by a second kernel where the tile grid is small: qkv / o / down at 100 and 256 rows,
 # o / down at 600)
-@pytest.mark.parametrize("B", [1, 2, 3, 16, 32, 64, 100, 256, 600])
+@pytest.mark.parametrize("B", [1, 2, 3, 16, 20, 32, 64, 100, 256, 600])
 @pytest.mark.parametrize("name", ["qkv", "o", "gu", "down"])
 def test_linear_epilogues(ops, name, B):
     say(f"linear {name} B={B}")
