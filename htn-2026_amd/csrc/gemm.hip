@@ -587,6 +587,10 @@ static int64_t gemm_mt(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, 
   // to the weight rows (measured 223 vs 238 us at 32 rows); the projections (10-76 rows per
   // workgroup) stay on the LDS-staged kernel, where the activation re-reads dominated
   if constexpr (EPI == EPI_ARGMAX) {
+    if (M <= 32) {
+      const int64_t parts = launch_lm_skinny(x, xs, M, w, N, K, pval, pidx, logits, s);
+      if (parts > 0) return parts;
+    }
     if (M <= 64 && K % 512 == 0 && aligned && P >= 1) {
       if (M <= 16) return stream_mt<1, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, P, s);
       if (M <= 32) return stream_mt<2, EPI>(x, xs, M, w, N, K, out, os, res, rs, pval, pidx, logits, P, s);

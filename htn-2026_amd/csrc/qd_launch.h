@@ -65,6 +65,10 @@ int64_t launch_gemm(const bf16_t* x, int64_t x_stride, int64_t M, const bf16_t* 
 bool skinny_ok(int64_t M, int64_t N, int64_t K, int epi, int S, const void* x, int64_t xs,
                const void* w, int64_t os);
 int64_t skinny_part_floats(int64_t M, int64_t N, int S);
+// LM head + argmax partials at <= 32 rows: returns the partials written per row (one per
+// workgroup, at most the CU count), or 0 when the shape is not supported (nothing launched)
+int64_t launch_lm_skinny(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
+                         int64_t K, float* pval, int32_t* pidx, float* logits, hipStream_t s);
 bool launch_gemm_skinny(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
                         int64_t K, int epi, int S, bf16_t* out, int64_t os, const bf16_t* res,
                         int64_t rs, float* part, hipStream_t s);
