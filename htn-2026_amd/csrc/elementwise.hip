@@ -239,13 +239,17 @@ __device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
 
 constexpr int QKR_ROWS = 4;   // token rows per workgroup: their loads are issued together
 
+// PART: the packed qkv rows are the split-K partials of the qkv projection, part[S][B*T][width]
+// fp32 (the tiled GEMM's split layout): each value is their sum in split order rounded to
+// bf16, the same bits gemm_split_reduce_kernel would have stored.
+template <bool PART>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const bf16_t* __restrict__ qkv, int64_t qkv_stride, const bf16_t* __restrict__ qn,
     const bf16_t* __restrict__ kn, const bf16_t* __restrict__ cos_t,
     const bf16_t* __restrict__ sin_t, int64_t table_len, const int64_t* __restrict__ pos,
     const int64_t* __restrict__ depth, int mode, bf16_t* __restrict__ q_out,
     bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache, int64_t T, int Hq, int Hkv,
-    int64_t cap, float eps) {
+    int64_t cap, float eps, const float* __restrict__ part, int S, int64_t rows_total) {
   // grid (token blocks of QKR_ROWS, sequence b, head group of 16): no integer division
   const int head = (int)blockIdx.z * 16 + (threadIdx.x >> 4);
   if (head >= Hq + 2 * Hkv) return;            // whole 16-lane groups leave together
@@ -254,10 +258,28 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   const int j = threadIdx.x & 15;
   const bool vhead = head >= Hq + Hkv, lo = j < 8;
   uint4 xr[QKR_ROWS];
+  if constexpr (PART) {
+    const int64_t width = (int64_t)(Hq + 2 * Hkv) * 128;
 #pragma unroll
-  for (int i = 0; i < QKR_ROWS; ++i) {         // every row's 16 bytes in flight at once
-    const int64_t t = t0 + i < T ? t0 + i : T - 1;
-    xr[i] = reinterpret_cast<const uint4*>(qkv + (b * T + t) * qkv_stride + (int64_t)head * 128)[j];
+    for (int i = 0; i < QKR_ROWS; ++i) {
+      const int64_t t = t0 + i < T ? t0 + i : T - 1;
+      const int64_t col = (b * T + t) * width + (int64_t)head * 128 + 8 * j;
+      const float4* p0 = reinterpret_cast<const float4*>(part + col);
+      float4 a = p0[0], c2 = p0[1];
+      for (int sp = 1; sp < S; ++sp) {
+        const float4* ps = reinterpret_cast<const float4*>(part + (int64_t)sp * rows_total * width + col);
+        const float4 a2 = ps[0], b2 = ps[1];
+        a.x += a2.x; a.y += a2.y; a.z += a2.z; a.w += a2.w;
+        c2.x += b2.x; c2.y += b2.y; c2.z += b2.z; c2.w += b2.w;
+      }
+      xr[i] = make_uint4(pack2(a.x, a.y), pack2(a.z, a.w), pack2(c2.x, c2.y), pack2(c2.z, c2.w));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < QKR_ROWS; ++i) {         // every row's 16 bytes in flight at once
+      const int64_t t = t0 + i < T ? t0 + i : T - 1;
+      xr[i] = reinterpret_cast<const uint4*>(qkv + (b * T + t) * qkv_stride + (int64_t)head * 128)[j];
+    }
   }
   const uint4 w = reinterpret_cast<const uint4*>(head < Hq ? qn : kn)[j];
 #pragma unroll
@@ -318,9 +340,23 @@ void launch_qk_norm_rope(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn
   if (B * T <= 0) return;
   const dim3 grid((unsigned)((T + QKR_ROWS - 1) / QKR_ROWS), (unsigned)B,
                   (unsigned)((Hq + 2 * Hkv + 15) / 16));
-  qk_norm_rope_kernel<<<grid, dim3(256), 0, s>>>(qkv, qkv_stride, qn, kn, cos_t, sin_t, table_len,
-                                                 pos, depth, mode, q_out, k_cache, v_cache, T, Hq,
-                                                 Hkv, cap, eps);
+  qk_norm_rope_kernel<false><<<grid, dim3(256), 0, s>>>(qkv, qkv_stride, qn, kn, cos_t, sin_t,
+                                                        table_len, pos, depth, mode, q_out, k_cache,
+                                                        v_cache, T, Hq, Hkv, cap, eps, nullptr, 1,
+                                                        B * T);
+}
+
+void launch_qk_norm_rope_part(const float* part, int S, const bf16_t* qn, const bf16_t* kn,
+                              const bf16_t* cos_t, const bf16_t* sin_t, int64_t table_len,
+                              const int64_t* pos, const int64_t* depth, int mode, bf16_t* q_out,
+                              bf16_t* k_cache, bf16_t* v_cache, int64_t B, int64_t T, int Hq,
+                              int Hkv, int64_t cap, float eps, hipStream_t s) {
+  if (B * T <= 0) return;
+  const dim3 grid((unsigned)((T + QKR_ROWS - 1) / QKR_ROWS), (unsigned)B,
+                  (unsigned)((Hq + 2 * Hkv + 15) / 16));
+  qk_norm_rope_kernel<true><<<grid, dim3(256), 0, s>>>(nullptr, 0, qn, kn, cos_t, sin_t, table_len,
+                                                       pos, depth, mode, q_out, k_cache, v_cache, T,
+                                                       Hq, Hkv, cap, eps, part, S, B * T);
 }
 
 // ------------------------------------------------------------------ SwiGLU

@@ -466,7 +466,8 @@ bool launch_gemm_skinny(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w,
 int64_t launch_lm_skinny(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
                          int64_t K, float* pval, int32_t* pidx, float* logits, hipStream_t s) {
   const int P = skinny_cus();
-  if (M < 1 || M > 32 || P < 1 || K % SKA_KP || N >= (1 << 30) || K >= (1 << 30)) return 0;
+  if (M < 1 || M > 32 || P < 1 || P > 1024 || K % SKA_KP || N >= (1 << 30) || K >= (1 << 30))
+    return 0;   // (the LM workspace holds at most 1024 partials per row beyond V / 16)
   if (xs % 8 || reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w) % 16) return 0;
   if (!x || !w || !pval || !pidx) return 0;
   const int64_t rows = (N + P - 1) / P;

@@ -354,6 +354,23 @@ int64_t gemm_tile_ws_floats(int64_t M, int64_t N, int64_t K, int epi) {
 
 int64_t gemm_tile_argmax_parts(int64_t N) { return N / TN; }
 
+int gemm_tile_partials(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
+                       int64_t K, float* part, int64_t part_floats, hipStream_t s) {
+  if (M < GEMM_TILE_MIN_M || !part ||
+      !gemm_tile_ok(M, N, K, EPI_NONE, x, xs, w, part, N, nullptr, 0))
+    return 0;
+  int splits = gemm_tile_splits(M, N, K, EPI_NONE);
+  if (splits <= 1 || part_floats < (int64_t)splits * M * N) return 0;
+  const int ksteps = (int)(K / TK);
+  const int ks_per = (ksteps + splits - 1) / splits;
+  splits = (ksteps + ks_per - 1) / ks_per;              // no empty split
+  const int64_t mblocks = (M + TM - 1) / TM, nblocks = tile_nblocks(N, EPI_NONE);
+  gemm_tile_kernel<EPI_NONE, true><<<dim3((unsigned)(mblocks * nblocks * splits)), dim3(256), 0, s>>>(
+      x, xs, (int)M, w, (int)N, (int)K, (int)mblocks, (int)nblocks, ks_per, nullptr, 0, nullptr,
+      0, nullptr, nullptr, nullptr, part);
+  return splits;
+}
+
 // Returns the number of argmax partials per row written (EPI_ARGMAX), else 0.
 int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
                          int64_t K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs, int epi,

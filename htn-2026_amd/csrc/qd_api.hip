@@ -53,8 +53,13 @@ LmWs carve_lm(Carver& c, int64_t rows, int64_t V, int64_t K) {
   LmWs l;
   const bool vec = gemv_supported(rows, K) && K == 2560;
   l.parts = vec ? lm_vec_parts(V) : gemm_argmax_parts(V);
-  l.val = c.take<float>(rows * l.parts);
-  l.idx = c.take<int32_t>(rows * l.parts);
+  // room for the partials of whichever LM-head kernel serves these rows: the vector path, the
+  // 16-row tiles, or one per workgroup of the skinny kernel (at most min(V, CU count))
+  int64_t cap_parts = gemm_argmax_parts(V);
+  if (lm_vec_parts(V) > cap_parts) cap_parts = lm_vec_parts(V);
+  if ((V < 1024 ? V : 1024) > cap_parts) cap_parts = V < 1024 ? V : 1024;
+  l.val = c.take<float>(rows * cap_parts);
+  l.idx = c.take<int32_t>(rows * cap_parts);
   l.xn = vec ? nullptr : c.take<bf16_t>(rows * K);
   return l;
 }
@@ -74,13 +79,18 @@ int lm_head(const bf16_t* x, int64_t x_stride, const bf16_t* w, int64_t V, int64
   return launched();
 }
 
-// LM head + argmax over `rows` already-normalised rows xn [rows, K] (the MFMA path)
-int lm_head_normed(const bf16_t* xn, const bf16_t* w, int64_t V, int64_t K, int64_t rows,
-                   int64_t* tok, int64_t* pos_inc, const LmWs& l, hipStream_t s) {
-  const int64_t parts = launch_gemm(xn, K, rows, w, V, K, nullptr, 0, nullptr, 0, EPI_ARGMAX,
+// LM head + argmax over `rows` already-normalised rows of xn (row stride xs; the MFMA path)
+int lm_head_normed_strided(const bf16_t* xn, int64_t xs, const bf16_t* w, int64_t V, int64_t K,
+                           int64_t rows, int64_t* tok, const LmWs& l, hipStream_t s,
+                           int64_t* pos_inc = nullptr) {
+  const int64_t parts = launch_gemm(xn, xs, rows, w, V, K, nullptr, 0, nullptr, 0, EPI_ARGMAX,
                                     l.val, l.idx, nullptr, s);
   launch_argmax_reduce(l.val, l.idx, parts, rows, tok, pos_inc, s);
   return launched();
+}
+int lm_head_normed(const bf16_t* xn, const bf16_t* w, int64_t V, int64_t K, int64_t rows,
+                   int64_t* tok, int64_t* pos_inc, const LmWs& l, hipStream_t s) {
+  return lm_head_normed_strided(xn, K, w, V, K, rows, tok, l, s, pos_inc);
 }
 
 bool weights_ok(const qd_weights* w) {
@@ -606,27 +616,59 @@ int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
   if (st->c_base && st->c_src && st->c_cnt)
     launch_kv_compact(st->k_cache, st->v_cache, w->n_layers, B, Hkv, cap, st->c_base, st->c_src,
                       st->c_cnt, T, s);
+  // Projections whose tile grid splits K (the tree-verification rows) leave fp32 partials and
+  // their consumer sums them in split order: q/k norm + RoPE for qkv, the residual add + RMSNorm
+  // for o and down -- the same bits as a split reduce kernel, one launch fewer each.
+  // `pend` = splits of down partials not yet folded into the residual x.
+  int pend = 0;
   launch_embed(st->tokens, w->embed, st->x, M, V, H, H, s);
   for (int64_t l = 0; l < w->n_layers; ++l) {
     bf16_t* kc = st->k_cache + l * layer_kv;
     bf16_t* vc = st->v_cache + l * layer_kv;
-    launch_add_rmsnorm(nullptr, st->x, w->ln1 + l * H, nullptr, st->xn, M, H, H, H, w->eps, s);
-    launch_gemm(st->xn, H, M, w->w_qkv + l * NQKV * H, NQKV, H, st->qkv, NQKV, nullptr, 0, EPI_NONE,
-                nullptr, nullptr, nullptr, s, part, part_floats);
-    launch_qk_norm_rope(st->qkv, NQKV, w->q_norm + l * 128, w->k_norm + l * 128, st->cos, st->sin,
-                        cap, st->base, st->depth, st->causal ? POS_CHUNK : POS_TREE, st->q, kc, vc,
-                        B, T, Hq, Hkv, cap, w->eps, s);
+    if (pend)
+      launch_part_add_rmsnorm(part, pend, M, st->x, w->ln1 + l * H, st->xn, H, w->eps, s);
+    else
+      launch_add_rmsnorm(nullptr, st->x, w->ln1 + l * H, nullptr, st->xn, M, H, H, H, w->eps, s);
+    const int sq = gemm_tile_partials(st->xn, H, M, w->w_qkv + l * NQKV * H, NQKV, H, part,
+                                      part_floats, s);
+    if (sq) {
+      launch_qk_norm_rope_part(part, sq, w->q_norm + l * 128, w->k_norm + l * 128, st->cos, st->sin,
+                               cap, st->base, st->depth, st->causal ? POS_CHUNK : POS_TREE, st->q,
+                               kc, vc, B, T, Hq, Hkv, cap, w->eps, s);
+    } else {
+      launch_gemm(st->xn, H, M, w->w_qkv + l * NQKV * H, NQKV, H, st->qkv, NQKV, nullptr, 0,
+                  EPI_NONE, nullptr, nullptr, nullptr, s, part, part_floats);
+      launch_qk_norm_rope(st->qkv, NQKV, w->q_norm + l * 128, w->k_norm + l * 128, st->cos,
+                          st->sin, cap, st->base, st->depth, st->causal ? POS_CHUNK : POS_TREE,
+                          st->q, kc, vc, B, T, Hq, Hkv, cap, w->eps, s);
+    }
     launch_block_attn(st->q, kc, vc, st->base, st->causal ? nullptr : st->anc, B, T, Hq, Hkv, cap,
                       splits, acc, ml, st->attn, s);
-    launch_gemm(st->attn, QD, M, w->w_o + l * H * QD, H, QD, st->x, H, st->x, H, EPI_RES, nullptr,
-                nullptr, nullptr, s, part, part_floats);
-    launch_add_rmsnorm(nullptr, st->x, w->ln2 + l * H, nullptr, st->xn, M, H, H, H, w->eps, s);
+    const int so = gemm_tile_partials(st->attn, QD, M, w->w_o + l * H * QD, H, QD, part,
+                                      part_floats, s);
+    if (so) {
+      launch_part_add_rmsnorm(part, so, M, st->x, w->ln2 + l * H, st->xn, H, w->eps, s);
+    } else {
+      launch_gemm(st->attn, QD, M, w->w_o + l * H * QD, H, QD, st->x, H, st->x, H, EPI_RES,
+                  nullptr, nullptr, nullptr, s, part, part_floats);
+      launch_add_rmsnorm(nullptr, st->x, w->ln2 + l * H, nullptr, st->xn, M, H, H, H, w->eps, s);
+    }
     launch_gemm(st->xn, H, M, w->w_gu + l * 2 * I * H, I, H, st->act, I, nullptr, 0, EPI_SWIGLU,
                 nullptr, nullptr, nullptr, s);
-    launch_gemm(st->act, I, M, w->w_down + l * H * I, H, I, st->x, H, st->x, H, EPI_RES, nullptr,
-                nullptr, nullptr, s, part, part_floats);
+    pend = gemm_tile_partials(st->act, I, M, w->w_down + l * H * I, H, I, part, part_floats, s);
+    if (!pend)
+      launch_gemm(st->act, I, M, w->w_down + l * H * I, H, I, st->x, H, st->x, H, EPI_RES, nullptr,
+                  nullptr, nullptr, s, part, part_floats);
   }
-  if (st->lm_mode == QD_LM_NONE) return launched();
+  if (st->lm_mode == QD_LM_NONE) return launched();   // K/V only (x is not read afterwards)
+  if (pend) {
+    // the last down partials: residual + final norm for every row, then the normalised rows
+    launch_part_add_rmsnorm(part, pend, M, st->x, w->final_norm, st->xn, H, w->eps, s);
+    if (st->lm_mode == QD_LM_LAST)
+      return lm_head_normed_strided(st->xn + (T - 1) * H, T * H, lm_weight(w), V, H, B,
+                                    st->out_tok, lw, s);
+    return lm_head_normed_strided(st->xn, H, lm_weight(w), V, H, M, st->out_tok, lw, s);
+  }
   if (st->lm_mode == QD_LM_LAST)
     return lm_head(st->x + (T - 1) * H, T * H, lm_weight(w), V, H, B, w->final_norm, w->eps,
                    st->out_tok, nullptr, nullptr, lw, s);

@@ -29,6 +29,12 @@ void launch_qk_norm_rope(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn
                          const int64_t* pos, const int64_t* depth, int mode, bf16_t* q_out,
                          bf16_t* k_cache, bf16_t* v_cache, int64_t B, int64_t T, int Hq, int Hkv,
                          int64_t cap, float eps, hipStream_t s);
+// the same with the qkv rows given as split-K partials part[S][B*T][(Hq + 2 Hkv) * 128] fp32
+void launch_qk_norm_rope_part(const float* part, int S, const bf16_t* qn, const bf16_t* kn,
+                              const bf16_t* cos_t, const bf16_t* sin_t, int64_t table_len,
+                              const int64_t* pos, const int64_t* depth, int mode, bf16_t* q_out,
+                              bf16_t* k_cache, bf16_t* v_cache, int64_t B, int64_t T, int Hq,
+                              int Hkv, int64_t cap, float eps, hipStream_t s);
 void launch_swiglu(const bf16_t* gu, int64_t gu_stride, bf16_t* out, int64_t out_stride,
                    int64_t rows, int64_t inter, hipStream_t s);
 void launch_kv_compact(bf16_t* k_all, bf16_t* v_all, int64_t L, int64_t B, int Hkv, int64_t cap,
@@ -72,7 +78,11 @@ int64_t launch_lm_skinny(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w
 bool launch_gemm_skinny(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
                         int64_t K, int epi, int S, bf16_t* out, int64_t os, const bf16_t* res,
                         int64_t rs, float* part, hipStream_t s);
-// gemm_tile.hip (LDS-tiled MFMA GEMM for M > 64)
+// gemm_tile.hip (LDS-tiled MFMA GEMM for M > 64).  gemm_tile_partials: when the tile grid
+// would split K, launch only the split kernel (fp32 partials part[S][M][N], no reduce) and
+// return S; otherwise launch nothing and return 0.
+int gemm_tile_partials(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
+                       int64_t K, float* part, int64_t part_floats, hipStream_t s);
 bool gemm_tile_ok(int64_t M, int64_t N, int64_t K, int epi, const void* x, int64_t x_stride,
                   const void* w, const void* out, int64_t out_stride, const void* res,
                   int64_t res_stride);
