@@ -213,31 +213,42 @@ void launch_add_rmsnorm(const bf16_t* x, const bf16_t* res, const bf16_t* w, bf1
 }
 
 // ------------------------------------------------------------------ q/k RMSNorm + RoPE + KV write
-// 16 lanes per (token row, head in [0, Hq + 2 Hkv)), 16 heads x 4 rows per workgroup: lane j
-// of a head holds dims 8j .. 8j+7 as one 16-byte load, so a wave moves 1 KiB per access and
-// the rotate_half partner of lane j (dims 64 apart) is lane j ^ 8 of the same DPP row.
+// 8 lanes per (token row, head in [0, Hq + 2 Hkv)): lane j holds dims 8j .. 8j+7 ("lo") and
+// their rotate_half partners 64 + 8j .. ("hi"), two 16-byte loads, so the pair terms of the
+// statistics and the rotation need no cross-lane moves and no lane computes a term twice.
+// A 256-thread workgroup is 32 such groups: 16 heads x 2 runs of QKR_RPG consecutive token
+// rows (one run per pair of waves, so row-dependent branches are wave-uniform).
 // Per-head RMSNorm (q_norm / k_norm weights), then
 //   o1 = bf16(bf16(y1 c1) + bf16(-y2 s1)),  o2 = bf16(bf16(y2 c2) + bf16(y1 s2))
 // for each (d, d + 64) pair (fused.py:24-81, tree.py:26-69, TF:modeling_qwen3.py:140-170,
 // 252-257).  The 64 sum-of-squares terms sq_pair(x_d, x_{d+64}) are added as a balanced binary
 // tree in index order -- within the lane over its 8 pairs, then across lanes j = 0..7 -- the
 // same tree wave_sum builds over lanes d = 0..63 in the decode attention unit, so the
-// statistics are bit-identical to the decode step's.  V heads are copied unnormalised into
-// the cache.  Position of token t of row b:
+// statistics are bit-identical to the decode step's.  rstd (an IEEE sqrt and divide) is
+// computed once per lane for row j & 3 of the lane's run and broadcast within each quad.
+// V heads are copied unnormalised into the cache.  Position of token t of row b:
 //   POS_T t | POS_SHARED pos[0]+t | POS_ROW pos[b]+t | POS_CHUNK pos[b]+t (= slot)
 //   POS_TREE: RoPE at pos[b] + depth[b*T + t], cache slot pos[b] + t.
-__device__ __forceinline__ uint32_t row_xor8(uint32_t v) {    // lane ^ 8 within a 16-lane row
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, true);   // row_ror:8
-}
-__device__ __forceinline__ uint4 row_xor8(const uint4 v) {
-  return make_uint4(row_xor8(v.x), row_xor8(v.y), row_xor8(v.z), row_xor8(v.w));
-}
 __device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
   f[0] = bflo(v.x); f[1] = bfhi(v.x); f[2] = bflo(v.y); f[3] = bfhi(v.y);
   f[4] = bflo(v.z); f[5] = bfhi(v.z); f[6] = bflo(v.w); f[7] = bfhi(v.w);
 }
+// two values rounded through bf16 with one conversion (the empty asm keeps the compiler from
+// splitting it back into one conversion per value)
+__device__ __forceinline__ void rbf2(float& a, float& b) {
+  uint32_t p = pack2(a, b);
+  asm("" : "+v"(p));
+  a = bflo(p);
+  b = bfhi(p);
+}
+// hide a packed word's origin from the optimiser, so values derived from it are recomputed
+// where they are used instead of being kept live from an earlier use
+__device__ __forceinline__ void opaque(uint4& v) {
+  asm("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
 
-constexpr int QKR_ROWS = 4;   // token rows per workgroup: their loads are issued together
+constexpr int QKR_RPG = 4;              // token rows per 8-lane group
+constexpr int QKR_ROWS = 2 * QKR_RPG;   // token rows per workgroup
 
 // PART: the packed qkv rows are the split-K partials of the qkv projection, part[S][B*T][width]
 // fp32 (the tiled GEMM's split layout): each value is their sum in split order rounded to
@@ -251,84 +262,166 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache, int64_t T, int Hq, int Hkv,
     int64_t cap, float eps, const float* __restrict__ part, int S, int64_t rows_total) {
   // grid (token blocks of QKR_ROWS, sequence b, head group of 16): no integer division
-  const int head = (int)blockIdx.z * 16 + (threadIdx.x >> 4);
-  if (head >= Hq + 2 * Hkv) return;            // whole 16-lane groups leave together
+  const int grp = threadIdx.x >> 3, j = threadIdx.x & 7;
+  const int head = (int)blockIdx.z * 16 + (grp & 15);
+  if (head >= Hq + 2 * Hkv) return;            // whole 8-lane groups leave together
   const int64_t b = blockIdx.y;
-  const int64_t t0 = (int64_t)blockIdx.x * QKR_ROWS;
-  const int j = threadIdx.x & 15;
-  const bool vhead = head >= Hq + Hkv, lo = j < 8;
-  uint4 xr[QKR_ROWS];
+  // the run's first row: uniform over the wave (waves 0-1 the first run, 2-3 the second), so
+  // every row-dependent value below lives in scalar registers
+  const int run = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 7);
+  const int64_t t0 = (int64_t)blockIdx.x * QKR_ROWS + run * QKR_RPG;
+  const bool vhead = head >= Hq + Hkv;
+  uint4 xl[QKR_RPG], xh[QKR_RPG];
   if constexpr (PART) {
     const int64_t width = (int64_t)(Hq + 2 * Hkv) * 128;
 #pragma unroll
-    for (int i = 0; i < QKR_ROWS; ++i) {
+    for (int i = 0; i < QKR_RPG; ++i) {
       const int64_t t = t0 + i < T ? t0 + i : T - 1;
       const int64_t col = (b * T + t) * width + (int64_t)head * 128 + 8 * j;
-      const float4* p0 = reinterpret_cast<const float4*>(part + col);
-      float4 a = p0[0], c2 = p0[1];
-      for (int sp = 1; sp < S; ++sp) {
-        const float4* ps = reinterpret_cast<const float4*>(part + (int64_t)sp * rows_total * width + col);
-        const float4 a2 = ps[0], b2 = ps[1];
-        a.x += a2.x; a.y += a2.y; a.z += a2.z; a.w += a2.w;
-        c2.x += b2.x; c2.y += b2.y; c2.z += b2.z; c2.w += b2.w;
+      float4 v[4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4* p0 = reinterpret_cast<const float4*>(part + col + 64 * h);
+        v[2 * h] = p0[0];
+        v[2 * h + 1] = p0[1];
       }
-      xr[i] = make_uint4(pack2(a.x, a.y), pack2(a.z, a.w), pack2(c2.x, c2.y), pack2(c2.z, c2.w));
+      for (int sp = 1; sp < S; ++sp) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float4* ps = reinterpret_cast<const float4*>(part + (int64_t)sp * rows_total * width + col + 64 * h);
+          const float4 a2 = ps[0], b2 = ps[1];
+          float4& a = v[2 * h];
+          float4& c = v[2 * h + 1];
+          a.x += a2.x; a.y += a2.y; a.z += a2.z; a.w += a2.w;
+          c.x += b2.x; c.y += b2.y; c.z += b2.z; c.w += b2.w;
+        }
+      }
+      xl[i] = make_uint4(pack2(v[0].x, v[0].y), pack2(v[0].z, v[0].w), pack2(v[1].x, v[1].y), pack2(v[1].z, v[1].w));
+      xh[i] = make_uint4(pack2(v[2].x, v[2].y), pack2(v[2].z, v[2].w), pack2(v[3].x, v[3].y), pack2(v[3].z, v[3].w));
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < QKR_ROWS; ++i) {         // every row's 16 bytes in flight at once
+    for (int i = 0; i < QKR_RPG; ++i) {          // every row's 2 x 16 bytes in flight at once
       const int64_t t = t0 + i < T ? t0 + i : T - 1;
-      xr[i] = reinterpret_cast<const uint4*>(qkv + (b * T + t) * qkv_stride + (int64_t)head * 128)[j];
+      const uint4* src = reinterpret_cast<const uint4*>(qkv + (b * T + t) * qkv_stride + (int64_t)head * 128);
+      xl[i] = src[j];
+      xh[i] = src[j + 8];
     }
   }
-  const uint4 w = reinterpret_cast<const uint4*>(head < Hq ? qn : kn)[j];
+  // positions (RoPE row, cache slot) of the run's rows
+  const int64_t p0 = mode == POS_T ? 0 : mode == POS_SHARED ? pos[0] : pos[b];
+  int64_t rpos[QKR_RPG], slot[QKR_RPG];
 #pragma unroll
-  for (int i = 0; i < QKR_ROWS; ++i) {
+  for (int i = 0; i < QKR_RPG; ++i) {
     const int64_t t = t0 + i;
-    if (t >= T) break;                         // uniform over the workgroup
-    const int64_t row = b * T + t;
-    int64_t rpos, slot;
-    switch (mode) {
-      case POS_T: rpos = slot = t; break;
-      case POS_SHARED: rpos = slot = pos[0] + t; break;
-      case POS_TREE: slot = pos[b] + t; rpos = pos[b] + depth[row]; break;
-      default: rpos = slot = pos[b] + t; break;  // POS_ROW, POS_CHUNK
+    slot[i] = p0 + t;
+    rpos[i] = mode == POS_TREE ? p0 + depth[b * T + (t < T ? t : T - 1)] : slot[i];
+  }
+  if (vhead) {                                 // V: copied into the cache as is
+    const int64_t base = (b * Hkv + (head - Hq - Hkv)) * cap;
+#pragma unroll
+    for (int i = 0; i < QKR_RPG; ++i) {
+      if (t0 + i >= T) break;                  // uniform over the wave
+      if (slot[i] < 0 || slot[i] >= cap) continue;
+      uint4* dst = reinterpret_cast<uint4*>(v_cache + (base + slot[i]) * 128);
+      dst[j] = xl[i];
+      dst[j + 8] = xh[i];
     }
-    const uint4 x = xr[i];
-    if (vhead) {                               // V: copied into the cache as is
-      if (slot >= 0 && slot < cap)
-        reinterpret_cast<uint4*>(v_cache + ((b * Hkv + (head - Hq - Hkv)) * cap + slot) * 128)[j] = x;
+    return;
+  }
+  // RoPE rows (clamped for the load; rows outside the table are skipped below): row i + 1's
+  // loads are issued when row i starts, so at most two rows of cos / sin are live
+  auto rope_row = [&](int i, uint4 (&cs)[4]) {
+    const int64_t r = rpos[i] < 0 ? 0 : (rpos[i] >= table_len ? table_len - 1 : rpos[i]);
+    const uint4* cr = reinterpret_cast<const uint4*>(cos_t + r * 128);
+    const uint4* sr = reinterpret_cast<const uint4*>(sin_t + r * 128);
+    cs[0] = cr[j]; cs[1] = cr[j + 8];
+    cs[2] = sr[j]; cs[3] = sr[j + 8];
+  };
+  uint4 csr[2][4];
+  rope_row(0, csr[0]);
+  float wl[8], wh[8];
+  {
+    const uint4* wsrc = reinterpret_cast<const uint4*>(head < Hq ? qn : kn);
+    unpack8(wsrc[j], wl);
+    unpack8(wsrc[j + 8], wh);
+  }
+  // statistics of every row of the run (all lanes active: DPP within the 8-lane group)
+  float tot[QKR_RPG];
+#pragma unroll
+  for (int i = 0; i < QKR_RPG; ++i) {
+    float a[8], c[8], sq[8];
+    unpack8(xl[i], a);
+    unpack8(xh[i], c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sq[e] = sq_pair(a[e], c[e]);
+    float s = ((sq[0] + sq[1]) + (sq[2] + sq[3])) + ((sq[4] + sq[5]) + (sq[6] + sq[7]));
+    s += QD_DPP(s, 0xB1);                      // lanes j ^ 1
+    s += QD_DPP(s, 0x4E);                      // lanes j ^ 2
+    s += QD_DPP(s, 0x141);                     // the other quad of the 8 (row_half_mirror)
+    tot[i] = s;
+  }
+#pragma unroll
+  for (int i = 0; i < QKR_RPG; ++i) { opaque(xl[i]); opaque(xh[i]); }   // unpacked again per row
+  // lane j computes rstd of row j & 3; quad_perm [i,i,i,i] hands row i's to every lane
+  const int q = j & 3;
+  const float tsel = q == 0 ? tot[0] : q == 1 ? tot[1] : q == 2 ? tot[2] : tot[3];
+  const float rq = rstd_of(tsel, 128, eps);
+  float rs[QKR_RPG];
+  rs[0] = QD_DPP(rq, 0x00);
+  rs[1] = QD_DPP(rq, 0x55);
+  rs[2] = QD_DPP(rq, 0xAA);
+  rs[3] = QD_DPP(rq, 0xFF);
+  static_assert(QKR_RPG == 4, "one row per quad lane");
+#pragma unroll
+  for (int i = 0; i < QKR_RPG; ++i) {
+    const int64_t t = t0 + i;
+    if (t >= T) break;                         // uniform over the wave
+    if (i + 1 < QKR_RPG) rope_row(i + 1, csr[(i + 1) & 1]);
+    __builtin_amdgcn_sched_barrier(0);         // keep the next row's loads here, not hoisted
+    if (rpos[i] < 0 || rpos[i] >= table_len) continue;
+    const int64_t row = b * T + t;
+    // one packed word (dims 2k, 2k + 1 of the lane's lo and hi runs) at a time, each closed by a
+    // scheduling barrier: interleaving all 16 dims would keep ~80 temporaries live and halve
+    // the waves a SIMD can hold
+    const uint32_t* X1 = reinterpret_cast<const uint32_t*>(&xl[i]);
+    const uint32_t* X2 = reinterpret_cast<const uint32_t*>(&xh[i]);
+    const uint32_t* C1 = reinterpret_cast<const uint32_t*>(&csr[i & 1][0]);
+    const uint32_t* C2 = reinterpret_cast<const uint32_t*>(&csr[i & 1][1]);
+    const uint32_t* S1 = reinterpret_cast<const uint32_t*>(&csr[i & 1][2]);
+    const uint32_t* S2 = reinterpret_cast<const uint32_t*>(&csr[i & 1][3]);
+    uint32_t ow[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      // norm: weight * bf16(x * rstd), rounded to bf16 (y1: the lo dims, y2: their partners)
+      float y1a = bflo(X1[k]) * rs[i], y1b = bfhi(X1[k]) * rs[i];
+      float y2a = bflo(X2[k]) * rs[i], y2b = bfhi(X2[k]) * rs[i];
+      rbf2(y1a, y1b); rbf2(y2a, y2b);
+      y1a *= wl[2 * k]; y1b *= wl[2 * k + 1];
+      y2a *= wh[2 * k]; y2b *= wh[2 * k + 1];
+      rbf2(y1a, y1b); rbf2(y2a, y2b);
+      // rotation: o1 = bf16(y1 c1) + bf16(-y2 s1), o2 = bf16(y2 c2) + bf16(y1 s2)
+      float p1a = y1a * bflo(C1[k]), p1b = y1b * bfhi(C1[k]);
+      float q1a = -y2a * bflo(S1[k]), q1b = -y2b * bfhi(S1[k]);
+      float p2a = y2a * bflo(C2[k]), p2b = y2b * bfhi(C2[k]);
+      float q2a = y1a * bflo(S2[k]), q2b = y1b * bfhi(S2[k]);
+      rbf2(p1a, p1b); rbf2(q1a, q1b); rbf2(p2a, p2b); rbf2(q2a, q2b);
+      ow[k] = pack2(p1a + q1a, p1b + q1b);
+      ow[4 + k] = pack2(p2a + q2a, p2b + q2b);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const uint4 ol = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    const uint4 oh = make_uint4(ow[4], ow[5], ow[6], ow[7]);
+    uint4* dst;
+    if (head < Hq) {
+      dst = reinterpret_cast<uint4*>(q_out + (row * Hq + head) * 128);   // q_out [B, T, Hq, 128]
+    } else if (slot[i] >= 0 && slot[i] < cap) {
+      dst = reinterpret_cast<uint4*>(k_cache + ((b * Hkv + (head - Hq)) * cap + slot[i]) * 128);
+    } else {
       continue;
     }
-    if (rpos < 0 || rpos >= table_len) continue;   // per row: the whole group
-    float xs[8], xp[8];
-    unpack8(x, xs);
-    unpack8(row_xor8(x), xp);                  // the partner dims (d +- 64)
-    float sq[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sq[e] = lo ? sq_pair(xs[e], xp[e]) : sq_pair(xp[e], xs[e]);
-    float tot = ((sq[0] + sq[1]) + (sq[2] + sq[3])) + ((sq[4] + sq[5]) + (sq[6] + sq[7]));
-    tot += QD_DPP(tot, 0xB1);                  // lanes j ^ 1
-    tot += QD_DPP(tot, 0x4E);                  // lanes j ^ 2
-    tot += QD_DPP(tot, 0x141);                 // the other 4-lane half of the 8 (row_half_mirror)
-    const float r = rstd_of(tot, 128, eps);
-    const uint4 y = norm8(x, w, r);            // bf16-rounded normed values of my dims
-    float ys[8], yp[8], c[8], sn[8];
-    unpack8(y, ys);
-    unpack8(row_xor8(y), yp);
-    unpack8(reinterpret_cast<const uint4*>(cos_t + rpos * 128)[j], c);
-    unpack8(reinterpret_cast<const uint4*>(sin_t + rpos * 128)[j], sn);
-    float o[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      o[e] = lo ? rbf(ys[e] * c[e]) + rbf(-yp[e] * sn[e]) : rbf(ys[e] * c[e]) + rbf(yp[e] * sn[e]);
-    const uint4 ov = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]),
-                                pack2(o[6], o[7]));
-    if (head < Hq) {
-      reinterpret_cast<uint4*>(q_out + (row * Hq + head) * 128)[j] = ov;   // q_out [B, T, Hq, 128]
-    } else if (slot >= 0 && slot < cap) {
-      reinterpret_cast<uint4*>(k_cache + ((b * Hkv + (head - Hq)) * cap + slot) * 128)[j] = ov;
-    }
+    dst[j] = ol;
+    dst[j + 8] = oh;
   }
 }
 
