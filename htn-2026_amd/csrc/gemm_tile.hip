@@ -28,6 +28,14 @@
 namespace {
 
 constexpr int TM = 128, TN = 128, TK = 64;
+#ifndef QD_TILE_RING
+#define QD_TILE_RING 2
+#endif
+// K stages of loads in flight per thread (even).  Measured on MI355X: 4 stages (250 VGPRs)
+// took 8.18 ms per config-5 verify forward against 8.01 ms with 2 and left the 4 x 8192
+// prefill unchanged -- the 256-row projections are not bound by load latency.
+constexpr int TILE_RING = QD_TILE_RING;
+static_assert(TILE_RING % 2 == 0, "the ring slots and the two LDS buffers advance together");
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
@@ -115,15 +123,15 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(
                 xrow_of(0), xrow_of(1), xrow_of(2), xrow_of(3)};
   uint4* lw0 = &sm.w[0][r0 * 8 + (unit0 ^ (r0 & 7))];              // + 256 i: rows + 32 i
   uint4* lx0 = &sm.x[0][r0 * 8 + (unit0 ^ (r0 & 7))];
-  Stage st0, st1;
+  Stage st[TILE_RING];
 // (the scheduling barrier keeps the loads at the head of the stage: left free, the scheduler
-// moves them behind the contraction and halves the prefetch distance)
-#define QD_LOAD(ST, KS)                                            \
+// moves them behind the contraction and shortens the prefetch distance)
+#define QD_LOAD(SLOT, KS)                                          \
   {                                                                \
-    load_stage(ST, src, ((KS) < kend ? (KS) : kend - 1) * 8);      \
+    load_stage(st[SLOT], src, ((KS) < kend ? (KS) : kend - 1) * 8);\
     __builtin_amdgcn_sched_barrier(0);                             \
   }
-#define QD_STORE(ST, BUF) store_stage(ST, lw0 + (BUF) * (TN * 8), lx0 + (BUF) * (TM * 8))
+#define QD_STORE(SLOT, BUF) store_stage(st[SLOT], lw0 + (BUF) * (TN * 8), lx0 + (BUF) * (TM * 8))
   f32x4_t acc[4][4];
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt)
@@ -142,26 +150,36 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(
                                                             acc[nt][mt], 0, 0, 0);             \
   }
 
-  // Stage s sits in LDS buffer s & 1 while the loads of stage s + 2 are in flight.  The loop
-  // body is a pair of stages with no exit between them (an exit there lets the compiler sink the
-  // first half's loads to their use, behind the contraction they are meant to overlap); an odd
-  // last stage is contracted after the loop.  Loads past the last stage are clamped to it.
-  QD_LOAD(st0, kbeg);
-  QD_LOAD(st1, kbeg + 1);
-  QD_STORE(st0, 0);
+  // Stage s sits in LDS buffer s & 1 while the loads of stages s + 1 .. s + TILE_RING are in
+  // flight in the register ring (slot s % TILE_RING is refilled with stage s + TILE_RING once
+  // stage s is in LDS).  Each stage: refill, contract, write stage s + 1 into the other buffer,
+  // one barrier.  The loop body is TILE_RING stages with no exit between them (an exit there lets
+  // the compiler sink loads to their use, behind the contraction they are meant to overlap);
+  // the last partial round is guarded stage by stage.  Loads past the last stage are clamped.
+#pragma unroll
+  for (int r = 0; r < TILE_RING; ++r) QD_LOAD(r, kbeg + r);
+  QD_STORE(0, 0);
   lds_barrier();
   int ks = kbeg;
-  for (; ks + 1 < kend; ks += 2) {
-    QD_LOAD(st0, ks + 2);
-    QD_COMPUTE(0);
-    QD_STORE(st1, 1);
-    lds_barrier();
-    QD_LOAD(st1, ks + 3);
-    QD_COMPUTE(1);
-    QD_STORE(st0, 0);
-    lds_barrier();
+  for (; ks + TILE_RING <= kend; ks += TILE_RING) {
+#pragma unroll
+    for (int r = 0; r < TILE_RING; ++r) {
+      QD_LOAD(r, ks + r + TILE_RING);
+      QD_COMPUTE(r & 1);
+      QD_STORE((r + 1) % TILE_RING, (r + 1) & 1);
+      lds_barrier();
+    }
   }
-  if (ks < kend) QD_COMPUTE(0);
+#pragma unroll
+  for (int r = 0; r < TILE_RING; ++r) {
+    if (ks + r < kend) {
+      QD_COMPUTE(r & 1);
+      if (ks + r + 1 < kend) {
+        QD_STORE((r + 1) % TILE_RING, (r + 1) & 1);
+        lds_barrier();
+      }
+    }
+  }
 #undef QD_LOAD
 #undef QD_STORE
 #undef QD_COMPUTE
