@@ -583,9 +583,10 @@ static int64_t gemm_mt(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, 
   const int P = stream_grid();
   const bool aligned = xs % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(w) % 16 == 0;
-  // the LM head: ~600 rows per workgroup, so the per-chunk activation re-reads are small next
-  // to the weight rows (measured 223 vs 238 us at 32 rows); the projections (10-76 rows per
-  // workgroup) stay on the LDS-staged kernel, where the activation re-reads dominated
+  // the LM head: 3..32 rows on the skinny argmax kernel (activations resident in LDS per K
+  // phase); 33..64 rows on the weight-streaming kernel (~600 rows per workgroup, so its per-chunk
+  // activation re-reads stay small next to the weight rows); the projections: 3..32 rows on the
+  // skinny kernel, 33..64 on the LDS-staged one
   if constexpr (EPI == EPI_ARGMAX) {
     if (M <= 32) {
       const int64_t parts = launch_lm_skinny(x, xs, M, w, N, K, pval, pidx, logits, s);
