@@ -36,6 +36,20 @@ constexpr int TM = 128, TN = 128, TK = 64;
 // prefill unchanged -- the 256-row projections are not bound by load latency.
 constexpr int TILE_RING = QD_TILE_RING;
 static_assert(TILE_RING % 2 == 0, "the ring slots and the two LDS buffers advance together");
+#ifndef QD_TILE_GROUP_M
+#define QD_TILE_GROUP_M 8
+#endif
+constexpr int TILE_GROUP_M = QD_TILE_GROUP_M;
+#ifndef QD_BIG_GROUP_M
+#define QD_BIG_GROUP_M 4
+#endif
+constexpr int BIG_GROUP_M = QD_BIG_GROUP_M;
+#ifndef QD_BIG_MIN_M
+#define QD_BIG_MIN_M 1024
+#endif
+#ifndef QD_BIG_EPIS
+#define QD_BIG_EPIS 7     // epilogues (bit EPI_NONE, EPI_RES, EPI_SWIGLU) that take the big tile
+#endif
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
@@ -90,9 +104,18 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(
   const int total = gridDim.x, h = blockIdx.x;
   const int xq = total >> 3, xr = total & 7, xcd = h & 7, slot = h >> 3;
   const int L = xcd < xr ? xcd * (xq + 1) + slot : xr * (xq + 1) + (xcd - xr) * xq + slot;
-  const int mb = L % mblocks;
-  const int nb = (L / mblocks) % nblocks;
-  const int split = L / (mblocks * nblocks);
+  // within a K split, tiles go in groups of TILE_GROUP_M M blocks: M fastest inside a group,
+  // then N, so the workgroups one XCD runs at a time cover a few M blocks x many N blocks and
+  // both the weight tiles and the activation tiles they read are shared in that XCD's L2
+  const int tiles = mblocks * nblocks;
+  const int split = L / tiles;
+  const int Lt = L - split * tiles;
+  const int group = Lt / (TILE_GROUP_M * nblocks);
+  const int first = group * TILE_GROUP_M;
+  const int gm = min(TILE_GROUP_M, mblocks - first);
+  const int rr = Lt - first * nblocks;
+  const int mb = first + rr % gm;
+  const int nb = rr / gm;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int c = lane & 15, q = lane >> 4;
@@ -320,6 +343,167 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
   *reinterpret_cast<uint2*>(out + m * out_stride + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
 }
 
+// ------------------------------------------------------------------ 256 x 256 tiles (prefill)
+// At prefill row counts (thousands of activation rows) the 128 x 128 tile above moves every
+// weight and activation byte through L1 once per 128 rows of the other operand (6.4 GB of
+// L1->L2 reads per 4096-row gate/up launch, a third of them L2 misses even with the grouped
+// tile order) and keeps the MFMA pipe 30 % busy.  This kernel doubles the tile both ways, halving
+// the traffic per flop: a workgroup of 8 waves (two per SIMD) owns 256 weight rows x 256
+// activation rows, wave (wm, wn) the 128 activation rows 128 wm .. x the 64 weight rows 64 wn ..
+// (4 x 8 MFMA tiles, 128 fp32 accumulators per lane, 224 VGPRs), K in stages of 64 through two
+// 64 KiB LDS buffers (16-byte units XOR-swizzled by row as above), one stage of loads in flight
+// (a stage is 64 MFMAs per wave).  Measured on MI355X at 4096 rows per launch: gate/up
+// 571 -> 412 us (991 TFLOP/s), qkv 188 -> 164 us, o / down 225 -> 203 us; with 4 waves of
+// 128 x 128 (256 accumulators each, one wave per SIMD) it was no faster than the small tile.
+// SwiGLU: a wave's 64 weight rows are 32 gate rows and the 32 up rows of the same outputs.
+constexpr int BT = 256;                      // weight rows and activation rows per workgroup
+
+struct BigLds {
+  uint4 w[2][BT * 8];
+  uint4 x[2][BT * 8];
+};
+
+// one stage of one thread's staging units: 4 weight and 4 activation 16-byte units
+struct BigStage {
+  uint4 w[4], x[4];
+};
+
+// 8 waves (two per SIMD): wave (wm, wn) owns activation rows 128 wm .. and weight rows 64 wn ..
+// (8 x 4 MFMA tiles, 128 accumulators per lane); SwiGLU: a wave's 64 weight rows are 32 gate
+// rows and the 32 up rows of the same outputs
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_big_kernel(
+    const bf16_t* __restrict__ X, int64_t x_stride, int M, const bf16_t* __restrict__ W, int N,
+    int K, int mblocks, int nblocks, bf16_t* out, int64_t out_stride, const bf16_t* res,
+    int64_t res_stride) {
+  __shared__ BigLds sm;
+  const int total = gridDim.x, h = blockIdx.x;
+  const int xq = total >> 3, xr = total & 7, xcd = h & 7, slot = h >> 3;
+  const int L = xcd < xr ? xcd * (xq + 1) + slot : xr * (xq + 1) + (xcd - xr) * xq + slot;
+  const int group = L / (BIG_GROUP_M * nblocks);
+  const int first = group * BIG_GROUP_M;
+  const int gm = min(BIG_GROUP_M, mblocks - first);
+  const int rr = L - first * nblocks;
+  const int mb = first + rr % gm;
+  const int nb = rr / gm;
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = lane & 15, q = lane >> 4;
+  const int wn = wave & 3, wm = wave >> 2;
+  const int64_t m0 = (int64_t)mb * BT;
+  const int ksteps = K / TK;
+  // staging: thread tid moves unit tid % 8 of LDS rows tid / 8 + 64 i (i < 4) of both tiles
+  const int r0 = tid >> 3, unit0 = tid & 7;
+  const int64_t kq = K / 8;                  // uint4 per row
+  const uint4* W4 = reinterpret_cast<const uint4*>(W);
+  const uint4* X4 = reinterpret_cast<const uint4*>(X);
+  // weight row of LDS row r0 + 64 i: plain nb*256 + r; SwiGLU: LDS rows [64 j, 64 j + 32) are
+  // the gate rows of outputs nb*128 + 32 j .., the next 32 the up rows (+ N) of the same outputs
+  auto wrow = [&](int i) -> int64_t {
+    if constexpr (EPI == EPI_SWIGLU) {       // LDS row r = r0 + 64 i: j = r / 64 = i, up = r0 >= 32
+      return (int64_t)nb * 128 + 32 * i + (r0 & 31) + (r0 >= 32 ? N : 0);
+    } else {
+      return (int64_t)nb * BT + r0 + 64 * i;
+    }
+  };
+  auto xrow = [&](int i) -> int64_t {
+    const int64_t m = m0 + r0 + 64 * i;
+    return m < M ? m : M - 1;
+  };
+  // 32-bit uint4 offsets (every operand here is < 2^32 16-byte units)
+  uint32_t wof[4], xof[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    wof[i] = (uint32_t)(wrow(i) * kq + unit0);
+    xof[i] = (uint32_t)(xrow(i) * (x_stride / 8) + unit0);
+  }
+  const int lofs = r0 * 8 + (unit0 ^ (r0 & 7));  // + 512 i: rows + 64 i (same swizzle)
+  BigStage st;
+  auto load = [&](int ks) {
+    const uint32_t kk = (uint32_t)ks * 8u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.w[i] = ld_stream(W4 + (wof[i] + kk));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.x[i] = X4[xof[i] + kk];
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sm.w[buf][lofs + 512 * i] = st.w[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sm.x[buf][lofs + 512 * i] = st.x[i];
+  };
+  f32x4_t acc[4][8];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int fa = (64 * wn + c) * 8, fb = (128 * wm + c) * 8;    // fragment rows (+ 128 t)
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int u = (4 * s + q) ^ (c & 7);
+      uint4 a[4], b[8];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) a[t] = sm.w[buf][fa + 128 * t + u];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) b[t] = sm.x[buf][fb + 128 * t + u];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt)
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(a[nt]), as_bf8(b[mt]),
+                                                                acc[nt][mt], 0, 0, 0);
+    }
+  };
+  // stage s in LDS buffer s & 1 while stage s + 1's loads are in flight
+  load(0);
+  store(0);
+  lds_barrier();
+  for (int ks = 0; ks < ksteps; ++ks) {
+    const bool more = ks + 1 < ksteps;       // uniform
+    if (more) load(ks + 1);
+    compute(ks & 1);
+    if (more) store((ks + 1) & 1);
+    lds_barrier();
+  }
+
+  // epilogue: lane (c, q) of acc[nt][mt] holds weight rows 4 q + r of tile nt = output columns
+  // n .. n + 3 of activation row m = m0 + 128 wm + 16 mt + c
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) {
+    const int64_t m = m0 + 128 * wm + 16 * mt + c;
+    if (m >= M) continue;
+    if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int64_t n = (int64_t)nb * 128 + 32 * wn + 16 * nt + 4 * q;
+        float y[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = rbf(silu_f(rbf(acc[nt][mt][r]))) * rbf(acc[nt + 2][mt][r]);
+        *reinterpret_cast<uint2*>(out + m * out_stride + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+      }
+    } else {
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int64_t n = (int64_t)nb * BT + 64 * wn + 16 * nt + 4 * q;
+        float y[4];
+        if constexpr (EPI == EPI_RES) {
+          const uint2 rv = *reinterpret_cast<const uint2*>(res + m * res_stride + n);
+          y[0] = bflo(rv.x) + rbf(acc[nt][mt][0]);
+          y[1] = bfhi(rv.x) + rbf(acc[nt][mt][1]);
+          y[2] = bflo(rv.y) + rbf(acc[nt][mt][2]);
+          y[3] = bfhi(rv.y) + rbf(acc[nt][mt][3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[r] = acc[nt][mt][r];
+        }
+        *reinterpret_cast<uint2*>(out + m * out_stride + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+      }
+    }
+  }
+}
+
 int64_t tile_nblocks(int64_t N, int epi) { return epi == EPI_SWIGLU ? N / 64 : N / TN; }
 
 }  // namespace
@@ -394,6 +578,18 @@ int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w
                          int64_t K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs, int epi,
                          float* pval, int32_t* pidx, float* logits, float* part,
                          int64_t part_floats, hipStream_t s) {
+  if (epi != EPI_ARGMAX && ((QD_BIG_EPIS >> epi) & 1) && M >= QD_BIG_MIN_M &&
+      (epi == EPI_SWIGLU ? N % 128 == 0 : N % BT == 0)) {
+    const int64_t mbl = (M + BT - 1) / BT, nbl = epi == EPI_SWIGLU ? N / 128 : N / BT;
+    const dim3 g((unsigned)(mbl * nbl)), b(512);
+#define QD_BIG(E) \
+  gemm_big_kernel<E><<<g, b, 0, s>>>(x, xs, (int)M, w, (int)N, (int)K, (int)mbl, (int)nbl, out, os, res, rs)
+    if (epi == EPI_RES) QD_BIG(EPI_RES);
+    else if (epi == EPI_SWIGLU) QD_BIG(EPI_SWIGLU);
+    else QD_BIG(EPI_NONE);
+#undef QD_BIG
+    return 0;
+  }
   const int64_t mblocks = (M + TM - 1) / TM, nblocks = tile_nblocks(N, epi);
   int splits = gemm_tile_splits(M, N, K, epi);
   if (splits > 1 && (!part || part_floats < (int64_t)splits * M * N)) splits = 1;

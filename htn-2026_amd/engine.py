@@ -46,7 +46,7 @@ class _Shape:
         cap = _model.kv_capacity(S, N, extra=tree_T)
         self.kv = _model.KVState(model, B, cap)
         self.stream = stream
-        self.chunk = _model.prefill_chunk(B, S, prefill_rows or 4096)
+        self.chunk = _model.prefill_chunk(B, S, prefill_rows or _model.PREFILL_ROWS)
         self.prefill = _model.BlockRunner(self.kv, stream, self.chunk, causal=True,
                                            lm_mode=_lib.LM_LAST)
         self.decode = _model.DecodeRunner(self.kv, stream, mega=mega)
@@ -96,7 +96,7 @@ class Engine:
         self.stream = torch.cuda.Stream(device=self.device)   # default priority
         self.shape = None
         self.tree_T = int(os.environ.get("ENGINE_TREE_T", "0"))
-        self.prefill_budget_rows = None    # rows per causal prefill chunk (None: 4096)
+        self.prefill_budget_rows = None    # rows per causal prefill chunk (None: PREFILL_ROWS)
         self.tree_stats = None
         self.tree_mode = TREE_MODE
         self.tree_on = {}                  # (B, S, N) -> the gate's decision
