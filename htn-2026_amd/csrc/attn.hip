@@ -121,7 +121,8 @@ static void launch_decode_attn_mfma(const bf16_t* qkv, int64_t qkv_stride, const
                                     const int64_t* pos, bf16_t* k_cache, bf16_t* v_cache,
                                     int64_t B, int Hq, int Hkv, int64_t cap, int64_t splits,
                                     int64_t chunk, float eps, float* ws_acc, float* ws_ml,
-                                    bf16_t* out, bool rope_row, hipStream_t s);
+                                    bf16_t* out, bool rope_row, hipStream_t s,
+                                    const float* part = nullptr, int part_S = 0);
 
 void launch_decode_attn(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn, const bf16_t* kn,
                         const bf16_t* cos_t, const bf16_t* sin_t, const int64_t* pos,
@@ -440,7 +441,7 @@ __global__ __launch_bounds__(DM_NW * 64) void decode_attn_mfma_kernel(
     const bf16_t* __restrict__ kn, const bf16_t* __restrict__ cos_t,
     const bf16_t* __restrict__ sin_t, const int64_t* __restrict__ pos_ptr, bf16_t* k_cache,
     bf16_t* v_cache, int Hq, int Hkv, int64_t cap, int64_t chunk, float eps, float scale,
-    float* ws_acc, float* ws_ml, bf16_t* out) {
+    float* ws_acc, float* ws_ml, bf16_t* out, const float* __restrict__ part, int part_S) {
   typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
   typedef __attribute__((ext_vector_type(4))) float f32x4_t;
   // 16-byte units as a native vector: copies of HIP's uint4 struct are memcpys, which keep the
@@ -471,11 +472,28 @@ __global__ __launch_bounds__(DM_NW * 64) void decode_attn_mfma_kernel(
   DM_LD(kx, vx, start + 32 * wave, cap);   // the wave's first tile, before pos is known
   // prologue loads: q head kvh * 4 + wave (waves 0..3; the others load it too and drop it);
   // wave 0 the new k, wave 1 the new v
-  const bf16_t* row = qkv + b * qkv_stride;
-  const bf16_t* qsrc = row + (int64_t)(kvh * GRP + (wave & (GRP - 1))) * 128;
-  const bf16_t* ksrc = row + (int64_t)(Hq + (wave == 1 ? Hkv : 0) + kvh) * 128;
-  const uint32_t q1 = qsrc[lane], q2 = qsrc[lane + 64];
-  const uint32_t k1 = ksrc[lane], k2 = ksrc[lane + 64];
+  const int64_t eq = (int64_t)(kvh * GRP + (wave & (GRP - 1))) * 128;
+  const int64_t ek = (int64_t)(Hq + (wave == 1 ? Hkv : 0) + kvh) * 128;
+  uint32_t q1, q2, k1, k2;
+  if (part) {
+    // the qkv projection's split-K partials part[S][B][W]: each value is their sum in split
+    // order rounded to bf16, the bits the projection's own epilogue stores when unsplit over
+    // the same order
+    const int64_t W = (int64_t)(Hq + 2 * Hkv) * 128;
+    const float* p0 = part + b * W;
+    float aq1 = p0[eq + lane], aq2 = p0[eq + lane + 64];
+    float ak1 = p0[ek + lane], ak2 = p0[ek + lane + 64];
+    for (int sp = 1; sp < part_S; ++sp) {
+      const float* ps = part + ((int64_t)sp * gridDim.z + b) * W;
+      aq1 += ps[eq + lane]; aq2 += ps[eq + lane + 64];
+      ak1 += ps[ek + lane]; ak2 += ps[ek + lane + 64];
+    }
+    q1 = f2bf(aq1); q2 = f2bf(aq2); k1 = f2bf(ak1); k2 = f2bf(ak2);
+  } else {
+    const bf16_t* row = qkv + b * qkv_stride;
+    q1 = row[eq + lane]; q2 = row[eq + lane + 64];
+    k1 = row[ek + lane]; k2 = row[ek + lane + 64];
+  }
   const float qw1 = bf2f(qn[lane]), qw2 = bf2f(qn[lane + 64]);
   const float kw1 = bf2f(kn[lane]), kw2 = bf2f(kn[lane + 64]);
   float c1, c2, s1, s2;
@@ -651,17 +669,32 @@ static void launch_decode_attn_mfma(const bf16_t* qkv, int64_t qkv_stride, const
                                     const int64_t* pos, bf16_t* k_cache, bf16_t* v_cache,
                                     int64_t B, int Hq, int Hkv, int64_t cap, int64_t splits,
                                     int64_t chunk, float eps, float* ws_acc, float* ws_ml,
-                                    bf16_t* out, bool rope_row, hipStream_t s) {
+                                    bf16_t* out, bool rope_row, hipStream_t s,
+                                    const float* part, int part_S) {
   const dim3 grid((unsigned)splits, (unsigned)Hkv, (unsigned)B), block(DM_NW * 64);
   const float scale = 1.0f / sqrtf(128.0f);
   if (rope_row)
     decode_attn_mfma_kernel<true><<<grid, block, 0, s>>>(qkv, qkv_stride, qn, kn, cos_t, sin_t,
                                                          pos, k_cache, v_cache, Hq, Hkv, cap,
-                                                         chunk, eps, scale, ws_acc, ws_ml, out);
+                                                         chunk, eps, scale, ws_acc, ws_ml, out,
+                                                         part, part_S);
   else
     decode_attn_mfma_kernel<false><<<grid, block, 0, s>>>(qkv, qkv_stride, qn, kn, cos_t, sin_t,
                                                           pos, k_cache, v_cache, Hq, Hkv, cap,
-                                                          chunk, eps, scale, ws_acc, ws_ml, out);
+                                                          chunk, eps, scale, ws_acc, ws_ml, out,
+                                                          part, part_S);
+}
+
+void launch_decode_attn_part(const float* part, int part_S, const bf16_t* qn, const bf16_t* kn,
+                             const bf16_t* cos_t, const bf16_t* sin_t, const int64_t* pos,
+                             bf16_t* k_cache, bf16_t* v_cache, int64_t B, int Hq, int Hkv,
+                             int64_t cap, int64_t splits, float eps, float* ws_acc, float* ws_ml,
+                             bf16_t* out, bool rope_row, hipStream_t s) {
+  const int64_t chunk = decode_attn_chunk(cap, splits);
+  launch_decode_attn_mfma(nullptr, 0, qn, kn, cos_t, sin_t, pos, k_cache, v_cache, B, Hq, Hkv,
+                          cap, splits, chunk, eps, ws_acc, ws_ml, out, rope_row, s, part, part_S);
+  if (splits > 1)
+    attn_merge_kernel<<<dim3((unsigned)(B * Hq)), dim3(64), 0, s>>>(ws_acc, ws_ml, (int)splits, out);
 }
 
 int64_t block_attn_splits(int64_t cap) { return (cap + BLOCK_CHUNK - 1) / BLOCK_CHUNK; }

@@ -104,16 +104,21 @@ bool weights_ok(const qd_weights* w) {
   return true;
 }
 
-// Batched decode (3..32 rows) on the skinny kernel: K splits of the o and down projections
-// (their partials are summed by the following residual-add + RMSNorm launch); qkv and gate/up
-// run unsplit.  Measured per projection at 32 rows on MI355X.
+// Batched decode (3..32 rows) on the skinny kernel: K splits of the qkv, o and down projections
+// (fewer activation bytes re-read per workgroup; the qkv partials are summed by the attention
+// prologue, the o / down partials by the following residual-add + RMSNorm launch); gate/up runs
+// unsplit (its SwiGLU epilogue needs whole sums).  Measured per projection at 32 rows on MI355X.
+#ifndef QD_SK_SPLIT_QKV
+#define QD_SK_SPLIT_QKV 2
+#endif
 #ifndef QD_SK_SPLIT_O
-#define QD_SK_SPLIT_O 2
+#define QD_SK_SPLIT_O 4
 #endif
 #ifndef QD_SK_SPLIT_DOWN
 #define QD_SK_SPLIT_DOWN 4
 #endif
-constexpr int SK_SPLIT_O = QD_SK_SPLIT_O, SK_SPLIT_DOWN = QD_SK_SPLIT_DOWN;
+constexpr int SK_SPLIT_QKV = QD_SK_SPLIT_QKV, SK_SPLIT_O = QD_SK_SPLIT_O,
+              SK_SPLIT_DOWN = QD_SK_SPLIT_DOWN;
 
 // Whether a B-row step runs the skinny path: shapes only (the workspace size depends on it), and
 // with a state, also the alignment of the step's own buffers (checked before anything launches)
@@ -124,7 +129,7 @@ bool skinny_step_ok(const qd_weights* w, int64_t B, const qd_decode_state* st = 
   const void* a = reinterpret_cast<const void*>(256);    // workspace regions: 256-aligned
   const void* attn = st ? st->attn : a;
   const void* act = st ? st->act : a;
-  return skinny_ok(B, NQKV, H, EPI_NONE, 1, a, H, st ? w->w_qkv : a, NQKV) &&
+  return skinny_ok(B, NQKV, H, EPI_NONE, SK_SPLIT_QKV, a, H, st ? w->w_qkv : a, NQKV) &&
          skinny_ok(B, H, QD, EPI_NONE, SK_SPLIT_O, attn, QD, st ? w->w_o : a, H) &&
          skinny_ok(B, I, H, EPI_SWIGLU, 1, a, H, st ? w->w_gu : a, I) &&
          skinny_ok(B, H, I, EPI_NONE, SK_SPLIT_DOWN, act, I, st ? w->w_down : a, H) &&
@@ -132,15 +137,20 @@ bool skinny_step_ok(const qd_weights* w, int64_t B, const qd_decode_state* st = 
                   reinterpret_cast<uintptr_t>(st->act) % 8 == 0));
 }
 
+inline int64_t qkv_width(const qd_weights* w) { return (int64_t)(w->n_q_heads + 2 * w->n_kv_heads) * 128; }
+
+// one partials buffer, reused: each projection's partials are consumed before the next
+// projection writes its own
 int64_t skinny_step_part_floats(const qd_weights* w, int64_t B) {
   const int S = SK_SPLIT_O > SK_SPLIT_DOWN ? SK_SPLIT_O : SK_SPLIT_DOWN;
-  return skinny_part_floats(B, w->hidden, S);
+  const int64_t od = skinny_part_floats(B, w->hidden, S);
+  const int64_t q = skinny_part_floats(B, qkv_width(w), SK_SPLIT_QKV);
+  return od > q ? od : q;
 }
 
 // the LM head's weight: the untied output projection when given, else the tied embedding
 inline const bf16_t* lm_weight(const qd_weights* w) { return w->lm_head ? w->lm_head : w->embed; }
 
-inline int64_t qkv_width(const qd_weights* w) { return (int64_t)(w->n_q_heads + 2 * w->n_kv_heads) * 128; }
 
 }  // namespace
 
@@ -400,12 +410,21 @@ int qd_decode_step(const qd_weights* w, const qd_decode_state* st, void* stream)
     for (int64_t l = 0; l < w->n_layers; ++l) {
       if (l > 0)
         launch_part_add_rmsnorm(part, SK_SPLIT_DOWN, B, st->x, w->ln1 + l * H, xn, H, w->eps, s);
-      launch_gemm_skinny(xn, H, B, w->w_qkv + l * NQKV * H, NQKV, H, EPI_NONE, 1, st->qkv, NQKV,
-                         nullptr, 0, nullptr, s);
-      launch_decode_attn(st->qkv, NQKV, w->q_norm + l * 128, w->k_norm + l * 128, rope_row,
-                         rope_row + 128, st->pos, st->k_cache + l * layer_kv,
-                         st->v_cache + l * layer_kv, B, Hq, Hkv, cap, splits, w->eps, aw.acc,
-                         aw.ml, st->attn, true, s);
+      if (SK_SPLIT_QKV > 1) {
+        launch_gemm_skinny(xn, H, B, w->w_qkv + l * NQKV * H, NQKV, H, EPI_NONE, SK_SPLIT_QKV,
+                           nullptr, 0, nullptr, 0, part, s);
+        launch_decode_attn_part(part, SK_SPLIT_QKV, w->q_norm + l * 128, w->k_norm + l * 128,
+                                rope_row, rope_row + 128, st->pos, st->k_cache + l * layer_kv,
+                                st->v_cache + l * layer_kv, B, Hq, Hkv, cap, splits, w->eps,
+                                aw.acc, aw.ml, st->attn, true, s);
+      } else {
+        launch_gemm_skinny(xn, H, B, w->w_qkv + l * NQKV * H, NQKV, H, EPI_NONE, 1, st->qkv,
+                           NQKV, nullptr, 0, nullptr, s);
+        launch_decode_attn(st->qkv, NQKV, w->q_norm + l * 128, w->k_norm + l * 128, rope_row,
+                           rope_row + 128, st->pos, st->k_cache + l * layer_kv,
+                           st->v_cache + l * layer_kv, B, Hq, Hkv, cap, splits, w->eps, aw.acc,
+                           aw.ml, st->attn, true, s);
+      }
       launch_gemm_skinny(st->attn, QD, B, w->w_o + l * H * QD, H, QD, EPI_NONE, SK_SPLIT_O,
                          nullptr, 0, nullptr, 0, part, s);
       launch_part_add_rmsnorm(part, SK_SPLIT_O, B, st->x, w->ln2 + l * H, xn, H, w->eps, s);

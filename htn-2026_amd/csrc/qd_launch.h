@@ -127,6 +127,13 @@ void launch_decode_attn(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn,
                         bf16_t* k_cache, bf16_t* v_cache, int64_t B, int Hq, int Hkv, int64_t cap,
                         int64_t splits, float eps, float* ws_acc, float* ws_ml, bf16_t* out,
                         bool rope_row, hipStream_t s);
+// B >= 2 decode attention whose q / k / v come from the qkv projection's split-K partials
+// part[part_S][B][(Hq + 2 Hkv) * 128] (fp32, summed in split order and rounded to bf16)
+void launch_decode_attn_part(const float* part, int part_S, const bf16_t* qn, const bf16_t* kn,
+                             const bf16_t* cos_t, const bf16_t* sin_t, const int64_t* pos,
+                             bf16_t* k_cache, bf16_t* v_cache, int64_t B, int Hq, int Hkv,
+                             int64_t cap, int64_t splits, float eps, float* ws_acc, float* ws_ml,
+                             bf16_t* out, bool rope_row, hipStream_t s);
 int64_t block_attn_splits(int64_t cap);
 void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
                        const int64_t* base, const uint64_t* anc, int64_t B, int64_t T, int Hq,
