@@ -407,10 +407,8 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
 // The decode unit (decode_attn_unit: same prologue, same numerics) with its two contractions on
 // v_mfma_f32_16x16x32_bf16.  Workgroup = (key split, KV head, sequence), 8 waves.  After the
 // prologue (q / k RMSNorm + RoPE, the new token's K/V written to the cache by the split that
-// owns pos), wave w takes 32-key tiles made of the 16-key units w + 16 i and w + 8 + 16 i of
-// the split's range, the new token included (balanced to within one unit across the waves:
-// 45.5 -> 45.0 us per layer at B = 32 against whole interleaved 32-key tiles): it stages each
-// tile key-major in its own LDS region (one 1 KiB-contiguous
+// owns pos), wave w takes tiles w, w + 8, ... of 32 keys of the split's range, the new token
+// included: it stages each tile key-major in its own LDS region (one 1 KiB-contiguous
 // non-temporal load per 4 keys, 16-byte units XOR-swizzled by key; the new token's row from
 // LDS) and contracts it as the block kernel does, with the group's 4 query heads as columns
 // 0..3 of the 16-column B operand: S' = K . Q^T, online softmax per column, O^T += V^T . P^T
@@ -459,23 +457,19 @@ __global__ __launch_bounds__(DM_NW * 64) void decode_attn_mfma_kernel(
   const u4v* kb = reinterpret_cast<const u4v*>(k_cache + head_off);
   const u4v* vb = reinterpret_cast<const u4v*>(v_cache + head_off);
   const int64_t start = (int64_t)split * chunk;
-  // Keys go in units of 16; a wave's 32-key tile i is the two units w + 16 i (keys 0..15 of the
-  // tile, from A0) and w + 8 + 16 i (keys 16..31, from A1), so every wave ends within one unit
-  // of the others (whole 32-key tiles left up to a tile of imbalance: 9 against 8.4 tiles per
-  // wave at a 2112-key context).
   // staging: lane moves 16-byte unit c of keys q4 + 4 j (j < 8) of a tile; keys at or past lim
   // reload row lim - 1 (a valid row, never attended as such)
   // one tile in flight per wave (registers), refilled as soon as the tile is staged
   u4v kx[8], vx[8];
-#define DM_LD(KX, VX, A0, A1, LIM)                                             \
+#define DM_LD(KX, VX, J0, LIM)                                                 \
   _Pragma("unroll") for (int dm_j_ = 0; dm_j_ < 8; ++dm_j_) {                  \
-    const int64_t dm_key_ = (dm_j_ < 4 ? (A0) : (A1)) + q4 + 4 * (dm_j_ & 3);  \
+    const int64_t dm_key_ = (J0) + q4 + 4 * dm_j_;                             \
     const int64_t dm_row_ = dm_key_ < (LIM) ? dm_key_ : (LIM) - 1;             \
     const int64_t dm_r_ = dm_row_ > 0 ? dm_row_ : 0;                           \
     KX[dm_j_] = __builtin_nontemporal_load(kb + dm_r_ * 16 + c);               \
     VX[dm_j_] = __builtin_nontemporal_load(vb + dm_r_ * 16 + c);               \
   }
-  DM_LD(kx, vx, start + 16 * wave, start + 16 * (wave + DM_NW), cap);   // before pos is known
+  DM_LD(kx, vx, start + 32 * wave, cap);   // the wave's first tile, before pos is known
   // prologue loads: q head kvh * 4 + wave (waves 0..3; the others load it too and drop it);
   // wave 0 the new k, wave 1 the new v
   const int64_t eq = (int64_t)(kvh * GRP + (wave & (GRP - 1))) * 128;
@@ -560,27 +554,25 @@ __global__ __launch_bounds__(DM_NW * 64) void decode_attn_mfma_kernel(
   f32x4_t o[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int units = kend > start ? (int)((kend - start + 15) / 16) : 0;
-  // stage the tile of units (a0, a1) from (kx_, vx_) into this wave's LDS region; the new
-  // token's row from LDS
-  auto stage = [&](const u4v (&kx_)[8], const u4v (&vx_)[8], int64_t a0, int64_t a1) {
+  const int ntiles = kend > start ? (int)((kend - start + 31) / 32) : 0;
+  // stage tile j0 from (kx_, vx_) into this wave's LDS region; the new token's row from LDS
+  auto stage = [&](const u4v (&kx_)[8], const u4v (&vx_)[8], int64_t j0) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int key = q4 + 4 * j;
       ks[key * 16 + (c ^ (key & 15))] = kx_[j];
       vs[key * 16 + (c ^ (key & 15))] = vx_[j];
     }
-    const int64_t p0 = pos - a0, p1 = pos - a1;
-    const int64_t pk = p0 >= 0 && p0 < 16 ? p0 : (p1 >= 0 && p1 < 16 ? 16 + p1 : -1);
-    if (pk >= 0 && q4 == 0) {                          // LDS keeps a wave's stores in order:
-      ks[pk * 16 + (c ^ (pk & 15))] = knew;            // this one wins
+    const int64_t pk = pos - j0;                       // LDS keeps a wave's stores in order:
+    if (pk >= 0 && pk < 32 && q4 == 0) {               // this one wins
+      ks[pk * 16 + (c ^ (pk & 15))] = knew;
       vs[pk * 16 + (c ^ (pk & 15))] = vnew;
     }
   };
   // contract the staged tile at j0 into (m, lsum, o).  The region is this wave's alone and LDS
   // serves a wave's accesses in order; the fences keep the compiler from moving fragment reads
   // above the staging stores, or the next staging above these reads.
-  auto contract = [&](int64_t a0, int64_t a1) {
+  auto contract = [&](int64_t j0) {
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     f32x4_t sc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -594,16 +586,14 @@ __global__ __launch_bounds__(DM_NW * 64) void decode_attn_mfma_kernel(
                                                         sc[h2], 0, 0, 0);
       }
     }
-    // lane (c, q4): scores of column c against keys 4 q4 + r of unit a0 (h2 = 0) and of unit
-    // a1 (h2 = 1); keys at or past kend are masked
-    const int64_t l0 = kend - a0, l1 = kend - a1;
-    const int lim0 = l0 < 16 ? (int)l0 : 16, lim1 = l1 < 16 ? (int)l1 : 16;
+    // lane (c, q4): scores of column c against keys 16 h2 + 4 q4 + r of the tile
+    const int lim = kend - j0 < 32 ? (int)(kend - j0) : 32;
     float sv[8];
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        sv[4 * h2 + r] = 4 * q4 + r < (h2 ? lim1 : lim0) ? sc[h2][r] * scale : NEG_INF;
+        sv[4 * h2 + r] = 16 * h2 + 4 * q4 + r < lim ? sc[h2][r] * scale : NEG_INF;
     float mx = sv[0];
 #pragma unroll
     for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
@@ -631,11 +621,11 @@ __global__ __launch_bounds__(DM_NW * 64) void decode_attn_mfma_kernel(
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   };
-  for (int u = wave; u < units; u += 2 * DM_NW) {
-    const int64_t a0 = start + 16 * (int64_t)u, a1 = a0 + 16 * DM_NW;
-    stage(kx, vx, a0, a1);
-    DM_LD(kx, vx, a0 + 32 * DM_NW, a1 + 32 * DM_NW, kend);   // the wave's next tile
-    contract(a0, a1);
+  for (int t = wave; t < ntiles; t += DM_NW) {
+    const int64_t j0 = start + 32 * (int64_t)t;
+    stage(kx, vx, j0);
+    DM_LD(kx, vx, j0 + 32 * DM_NW, kend);   // the wave's next tile
+    contract(j0);
   }
 #undef DM_LD
   // column totals (the four q4 lanes of a column hold disjoint keys), then the waves' states
