@@ -152,9 +152,13 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
 // end here): acc = sum of part[s][row] in split order (fp32), r' = bf16(res + bf16(acc))
 // written back to res -- the residual epilogue's rounding points (gemv.py:50-51) -- and
 // y = bf16(bf16(r' * rstd) * w).  One workgroup per row, hidden <= 8192.
+// SC > 0: the split count as a compile-time constant, so every split's loads are issued before
+// the first add (a runtime loop costs one round trip per split: 4.9 us per launch at 4 splits)
+template <int SC>
 __global__ __launch_bounds__(256) void part_add_rmsnorm_kernel(
-    const float* __restrict__ part, int S, int64_t rows, bf16_t* res, const bf16_t* __restrict__ w,
+    const float* __restrict__ part, int S_rt, int64_t rows, bf16_t* res, const bf16_t* __restrict__ w,
     bf16_t* __restrict__ y, int64_t hidden, float eps) {
+  const int S = SC > 0 ? SC : S_rt;
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   const int64_t nch = hidden / 8;
@@ -169,11 +173,27 @@ __global__ __launch_bounds__(256) void part_add_rmsnorm_kernel(
     if (c < nch) {
       const float4* p = reinterpret_cast<const float4*>(part + row * hidden) + 2 * c;
       float4 a = p[0], b = p[1];
-      for (int s = 1; s < S; ++s) {
-        const float4* ps = reinterpret_cast<const float4*>(part + ((int64_t)s * rows + row) * hidden) + 2 * c;
-        const float4 a2 = ps[0], b2 = ps[1];
-        a.x += a2.x; a.y += a2.y; a.z += a2.z; a.w += a2.w;
-        b.x += b2.x; b.y += b2.y; b.z += b2.z; b.w += b2.w;
+      if constexpr (SC > 0) {
+        float4 pa[SC > 1 ? SC - 1 : 1], pb[SC > 1 ? SC - 1 : 1];
+#pragma unroll
+        for (int s = 1; s < SC; ++s) {
+          const float4* ps = reinterpret_cast<const float4*>(part + ((int64_t)s * rows + row) * hidden) + 2 * c;
+          pa[s - 1] = ps[0];
+          pb[s - 1] = ps[1];
+        }
+#pragma unroll
+        for (int s = 1; s < SC; ++s) {
+          const float4 a2 = pa[s - 1], b2 = pb[s - 1];
+          a.x += a2.x; a.y += a2.y; a.z += a2.z; a.w += a2.w;
+          b.x += b2.x; b.y += b2.y; b.z += b2.z; b.w += b2.w;
+        }
+      } else {
+        for (int s = 1; s < S; ++s) {
+          const float4* ps = reinterpret_cast<const float4*>(part + ((int64_t)s * rows + row) * hidden) + 2 * c;
+          const float4 a2 = ps[0], b2 = ps[1];
+          a.x += a2.x; a.y += a2.y; a.z += a2.z; a.w += a2.w;
+          b.x += b2.x; b.y += b2.y; b.z += b2.z; b.w += b2.w;
+        }
       }
       const uint4 r = rr[c];
       uint4 o;
@@ -200,8 +220,14 @@ __global__ __launch_bounds__(256) void part_add_rmsnorm_kernel(
 void launch_part_add_rmsnorm(const float* part, int S, int64_t rows, bf16_t* res, const bf16_t* w,
                              bf16_t* y, int64_t hidden, float eps, hipStream_t s) {
   if (rows <= 0) return;
-  part_add_rmsnorm_kernel<<<dim3((unsigned)rows), dim3(256), 0, s>>>(part, S, rows, res, w, y,
-                                                                      hidden, eps);
+  const dim3 g((unsigned)rows), b(256);
+  switch (S) {
+    case 1: part_add_rmsnorm_kernel<1><<<g, b, 0, s>>>(part, S, rows, res, w, y, hidden, eps); break;
+    case 2: part_add_rmsnorm_kernel<2><<<g, b, 0, s>>>(part, S, rows, res, w, y, hidden, eps); break;
+    case 4: part_add_rmsnorm_kernel<4><<<g, b, 0, s>>>(part, S, rows, res, w, y, hidden, eps); break;
+    case 6: part_add_rmsnorm_kernel<6><<<g, b, 0, s>>>(part, S, rows, res, w, y, hidden, eps); break;
+    default: part_add_rmsnorm_kernel<0><<<g, b, 0, s>>>(part, S, rows, res, w, y, hidden, eps); break;
+  }
 }
 
 void launch_add_rmsnorm(const bf16_t* x, const bf16_t* res, const bf16_t* w, bf16_t* res_out,
