@@ -44,6 +44,9 @@ constexpr int TILE_GROUP_M = QD_TILE_GROUP_M;
 #define QD_BIG_GROUP_M 8
 #endif
 constexpr int BIG_GROUP_M = QD_BIG_GROUP_M;
+#ifndef QD_TILE8
+#define QD_TILE8 1        // 8-wave 128 x 128 tiles below the 256 x 256 kernel's row count
+#endif
 #ifndef QD_BIG_MIN_M
 #define QD_BIG_MIN_M 1024
 #endif
@@ -299,6 +302,160 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(
           *reinterpret_cast<uint2*>(out + m * out_stride + n) =
               make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
         }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ 128 x 128 tiles, 8 waves
+// The same tile, K stages, LDS layout, remap and split-K as gemm_tile_kernel, with 8 waves per
+// workgroup instead of 4: wave (wm, wn) owns activation rows 64 wm .. x weight rows 32 wn ..
+// (4 x 2 MFMA tiles), so each SIMD holds two waves of one workgroup (four when two workgroups
+// share a CU) to overlap one wave's loads and LDS traffic with another's MFMAs.  SwiGLU: a
+// wave's 32 weight rows are 16 gate rows and the 16 up rows of the same outputs.
+struct Stage8 {
+  uint4 w0, w1, x0, x1;
+};
+
+template <int EPI, bool SPLIT>
+__global__ __launch_bounds__(512, 2) void gemm_tile8_kernel(
+    const bf16_t* __restrict__ X, int64_t x_stride, int M, const bf16_t* __restrict__ W, int N,
+    int K, int mblocks, int nblocks, int ks_per, bf16_t* out, int64_t out_stride, const bf16_t* res,
+    int64_t res_stride, float* part) {
+  static_assert(EPI != EPI_ARGMAX, "the LM head keeps the 4-wave kernel");
+  __shared__ TileLds sm;
+  const int total = gridDim.x, h = blockIdx.x;
+  const int xq = total >> 3, xr = total & 7, xcd = h & 7, slot = h >> 3;
+  const int L = xcd < xr ? xcd * (xq + 1) + slot : xr * (xq + 1) + (xcd - xr) * xq + slot;
+  const int tiles = mblocks * nblocks;
+  const int split = L / tiles;
+  const int Lt = L - split * tiles;
+  const int group = Lt / (TILE_GROUP_M * nblocks);
+  const int first = group * TILE_GROUP_M;
+  const int gm = min(TILE_GROUP_M, mblocks - first);
+  const int rr = Lt - first * nblocks;
+  const int mb = first + rr % gm;
+  const int nb = rr / gm;
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = lane & 15, q = lane >> 4;
+  const int wn = wave & 3, wm = wave >> 2;
+  const int64_t m0 = (int64_t)mb * TM;
+  const int ksteps = K / TK;
+  const int kbeg = split * ks_per;
+  const int kend = min(ksteps, kbeg + ks_per);
+
+  // staging: thread tid moves unit tid % 8 of LDS rows r0 + 64 i (r0 = tid / 8, i < 2) of both
+  // tiles.  Weight row of LDS row R: nb*128 + R, or for SwiGLU nb*64 + 16 (R / 32) + R % 16,
+  // plus N when (R / 16) is odd (the up rows)
+  const int r0 = tid >> 3, unit0 = tid & 7;
+  const int Nrows = EPI == EPI_SWIGLU ? 2 * N : N;
+  auto wrow_of = [&](int i) -> int64_t {
+    const int R = r0 + 64 * i;
+    const int64_t wr = EPI == EPI_SWIGLU
+                           ? (int64_t)nb * 64 + 16 * (R >> 5) + (R & 15) + (((R >> 4) & 1) ? N : 0)
+                           : (int64_t)nb * TN + R;
+    return (wr < Nrows ? wr : Nrows - 1) * (K / 8) + unit0;          // in uint4 units
+  };
+  auto xrow_of = [&](int i) -> int64_t {
+    const int64_t xm = m0 + r0 + 64 * i;
+    return (xm < M ? xm : M - 1) * (x_stride / 8) + unit0;
+  };
+  const uint4* W4 = reinterpret_cast<const uint4*>(W);
+  const uint4* X4 = reinterpret_cast<const uint4*>(X);
+  const int64_t wo0 = wrow_of(0), wo1 = wrow_of(1), xo0 = xrow_of(0), xo1 = xrow_of(1);
+  uint4* lw0 = &sm.w[0][r0 * 8 + (unit0 ^ (r0 & 7))];              // + 512: rows + 64
+  uint4* lx0 = &sm.x[0][r0 * 8 + (unit0 ^ (r0 & 7))];
+  Stage8 st0, st1;
+  auto load = [&](Stage8& st, int ks) {
+    const int64_t kk = (int64_t)(ks < kend ? ks : kend - 1) * 8;
+    st.w0 = ld_stream(W4 + wo0 + kk);
+    st.w1 = ld_stream(W4 + wo1 + kk);
+    st.x0 = X4[xo0 + kk];
+    st.x1 = X4[xo1 + kk];
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto store = [&](const Stage8& st, int buf) {
+    lw0[buf * (TN * 8)] = st.w0;
+    lw0[buf * (TN * 8) + 512] = st.w1;
+    lx0[buf * (TM * 8)] = st.x0;
+    lx0[buf * (TM * 8) + 512] = st.x1;
+  };
+  f32x4_t acc[2][4];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int fa = (32 * wn + c) * 8, fb = (64 * wm + c) * 8;           // fragment rows (+ 128 t)
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int s_ = 0; s_ < 2; ++s_) {
+      const int u_ = (4 * s_ + q) ^ (c & 7);
+      uint4 a_[2], b_[4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) a_[t] = sm.w[buf][fa + 128 * t + u_];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) b_[t] = sm.x[buf][fb + 128 * t + u_];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(a_[nt]), as_bf8(b_[mt]),
+                                                                acc[nt][mt], 0, 0, 0);
+    }
+  };
+  // as gemm_tile_kernel: stage s in LDS buffer s & 1, loads of stages s + 1, s + 2 in flight
+  load(st0, kbeg);
+  load(st1, kbeg + 1);
+  store(st0, 0);
+  lds_barrier();
+  int ks = kbeg;
+  for (; ks + 1 < kend; ks += 2) {
+    load(st0, ks + 2);
+    compute(0);
+    store(st1, 1);
+    lds_barrier();
+    load(st1, ks + 3);
+    compute(1);
+    store(st0, 0);
+    lds_barrier();
+  }
+  if (ks < kend) compute(0);
+
+  // epilogue: lane (c, q) of acc[nt][mt] holds weight rows 4 q + r of tile nt = output columns
+  // n .. n + 3 of activation row m = m0 + 64 wm + 16 mt + c
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int64_t m = m0 + 64 * wm + 16 * mt + c;
+    if (m >= M) continue;
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int64_t n = (int64_t)nb * TN + 32 * wn + 16 * nt + 4 * q;
+        *reinterpret_cast<f32x4_t*>(part + ((int64_t)split * M + m) * N + n) = acc[nt][mt];
+      }
+    } else if constexpr (EPI == EPI_SWIGLU) {
+      const int64_t n = (int64_t)nb * 64 + 16 * wn + 4 * q;
+      float y[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) y[r] = rbf(silu_f(rbf(acc[0][mt][r]))) * rbf(acc[1][mt][r]);
+      *reinterpret_cast<uint2*>(out + m * out_stride + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+    } else {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int64_t n = (int64_t)nb * TN + 32 * wn + 16 * nt + 4 * q;
+        float y[4];
+        if constexpr (EPI == EPI_RES) {
+          const uint2 rv = *reinterpret_cast<const uint2*>(res + m * res_stride + n);
+          y[0] = bflo(rv.x) + rbf(acc[nt][mt][0]);
+          y[1] = bfhi(rv.x) + rbf(acc[nt][mt][1]);
+          y[2] = bflo(rv.y) + rbf(acc[nt][mt][2]);
+          y[3] = bfhi(rv.y) + rbf(acc[nt][mt][3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[r] = acc[nt][mt][r];
+        }
+        *reinterpret_cast<uint2*>(out + m * out_stride + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
       }
     }
   }
@@ -568,9 +725,14 @@ int gemm_tile_partials(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, 
   const int ks_per = (ksteps + splits - 1) / splits;
   splits = (ksteps + ks_per - 1) / ks_per;              // no empty split
   const int64_t mblocks = (M + TM - 1) / TM, nblocks = tile_nblocks(N, EPI_NONE);
-  gemm_tile_kernel<EPI_NONE, true><<<dim3((unsigned)(mblocks * nblocks * splits)), dim3(256), 0, s>>>(
-      x, xs, (int)M, w, (int)N, (int)K, (int)mblocks, (int)nblocks, ks_per, nullptr, 0, nullptr,
-      0, nullptr, nullptr, nullptr, part);
+  if (QD_TILE8)
+    gemm_tile8_kernel<EPI_NONE, true><<<dim3((unsigned)(mblocks * nblocks * splits)), dim3(512), 0, s>>>(
+        x, xs, (int)M, w, (int)N, (int)K, (int)mblocks, (int)nblocks, ks_per, nullptr, 0, nullptr,
+        0, part);
+  else
+    gemm_tile_kernel<EPI_NONE, true><<<dim3((unsigned)(mblocks * nblocks * splits)), dim3(256), 0, s>>>(
+        x, xs, (int)M, w, (int)N, (int)K, (int)mblocks, (int)nblocks, ks_per, nullptr, 0, nullptr,
+        0, nullptr, nullptr, nullptr, part);
   return splits;
 }
 
@@ -600,8 +762,14 @@ int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w
   const dim3 grid((unsigned)(mblocks * nblocks * splits)), block(256);
   const int Mi = (int)M, Ni = (int)N, Ki = (int)K, mbi = (int)mblocks, nbi = (int)nblocks;
 #define QD_TILE(E, SP)                                                                           \
-  gemm_tile_kernel<E, SP><<<grid, block, 0, s>>>(x, xs, Mi, w, Ni, Ki, mbi, nbi, ks_per, out, os, \
-                                                 res, rs, pval, pidx, logits, part)
+  do {                                                                                           \
+    if (QD_TILE8 && E != EPI_ARGMAX)                                                             \
+      gemm_tile8_kernel<E == EPI_ARGMAX ? EPI_NONE : E, SP><<<grid, dim3(512), 0, s>>>(          \
+          x, xs, Mi, w, Ni, Ki, mbi, nbi, ks_per, out, os, res, rs, part);                       \
+    else                                                                                         \
+      gemm_tile_kernel<E, SP><<<grid, block, 0, s>>>(x, xs, Mi, w, Ni, Ki, mbi, nbi, ks_per, out, \
+                                                     os, res, rs, pval, pidx, logits, part);     \
+  } while (0)
   if (splits > 1) {
     if (epi == EPI_RES) QD_TILE(EPI_RES, true);
     else QD_TILE(EPI_NONE, true);
