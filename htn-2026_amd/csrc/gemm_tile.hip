@@ -507,33 +507,71 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
 // tile order) and keeps the MFMA pipe 30 % busy.  This kernel doubles the tile both ways, halving
 // the traffic per flop: a workgroup of 8 waves (two per SIMD) owns 256 weight rows x 256
 // activation rows, wave (wm, wn) the 128 activation rows 128 wm .. x the 64 weight rows 64 wn ..
-// (4 x 8 MFMA tiles, 128 fp32 accumulators per lane, 224 VGPRs), K in stages of 64 through two
-// 64 KiB LDS buffers (16-byte units XOR-swizzled by row as above), one stage of loads in flight
-// (a stage is 64 MFMAs per wave).  Measured on MI355X at 4096 rows per launch: gate/up
-// 571 -> 412 us (991 TFLOP/s), qkv 188 -> 164 us, o / down 225 -> 203 us; with 4 waves of
-// 128 x 128 (256 accumulators each, one wave per SIMD) it was no faster than the small tile.
+// (4 x 8 MFMA tiles, 128 fp32 accumulators per lane).  K advances in stages of 32 that go from
+// global memory straight into LDS (global_load_lds_dwordx4: no staging registers, no LDS store
+// instructions), BIG_NBUF stage buffers of 32 KiB with BIG_NBUF - 1 stages in flight: with the
+// loads staged through registers only one 64-deep stage fitted in flight, and a copy of that
+// kernel without its MFMAs (loads, LDS stores and barriers only) took 539 us of the full
+// kernel's 714 us for a 6144-row gate/up -- bound by the load round trip, not the MFMA pipe.
 // SwiGLU: a wave's 64 weight rows are 32 gate rows and the 32 up rows of the same outputs.
 constexpr int BT = 256;                      // weight rows and activation rows per workgroup
+constexpr int BK = 32;                       // K per stage: 64 bytes of every row
+#ifndef QD_BIG_NBUF
+#define QD_BIG_NBUF 4
+#endif
+constexpr int BIG_NBUF = QD_BIG_NBUF;        // LDS stage buffers (BIG_NBUF x 32 KiB <= 160 KiB)
+static_assert(BIG_NBUF >= 2 && BIG_NBUF <= 5, "stage buffers");
 
-struct BigLds {
-  uint4 w[2][BT * 8];
-  uint4 x[2][BT * 8];
-};
+// LDS byte address of a __shared__ object
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// lane l's 16 bytes at base + voff go to LDS byte lds + 16 l (wave-uniform lds).  Issued as
+// inline asm so that the compiler, which would otherwise wait for every outstanding LDS DMA
+// before any later LDS read, leaves the waits to the explicit vmcnt counts of the stage loop.
+// The s_nop keeps a wait state between the compiler's M0 write and the load.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds)
+               : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// wait until at most PER * C of this wave's loads are outstanding, C = min(n, CMAX)
+template <int PER, int CMAX>
+__device__ __forceinline__ void wait_stages(int n) {
+  if constexpr (CMAX == 0) {
+    wait_vm<0>();
+  } else {
+    if (n >= CMAX) wait_vm<PER * CMAX>();
+    else wait_stages<PER, CMAX - 1>(n);
+  }
+}
 
-// one stage of one thread's staging units: 4 weight and 4 activation 16-byte units
-struct BigStage {
-  uint4 w[4], x[4];
-};
-
-// 8 waves (two per SIMD): wave (wm, wn) owns activation rows 128 wm .. and weight rows 64 wn ..
-// (8 x 4 MFMA tiles, 128 accumulators per lane); SwiGLU: a wave's 64 weight rows are 32 gate
-// rows and the 32 up rows of the same outputs
+// 8 waves (two per SIMD), two along the activation rows and four along the weight rows: wave
+// (wm, wn) owns activation rows 128 wm .. and weight rows 64 wn .. (8 x 4 MFMA tiles, 128 fp32
+// accumulators per lane).  SwiGLU: a wave's 64 weight rows are 32 gate rows and the 32 up rows
+// of the same outputs.  Offsets are 32-bit (checked by the launcher).  (Four waves of 128 x 128,
+// one per SIMD as in hipBLASLt's 256 x 256 tiles, need their 256 accumulators in the AGPRs; with
+// the fragment double buffer below the compiler spilled 241 registers.)
+constexpr int BIG_WAVES = 8;
 template <int EPI>
-__global__ __launch_bounds__(512, 1) void gemm_big_kernel(
+__global__ __launch_bounds__(BIG_WAVES * 64, 1) void gemm_big_kernel(
     const bf16_t* __restrict__ X, int64_t x_stride, int M, const bf16_t* __restrict__ W, int N,
     int K, int mblocks, int nblocks, bf16_t* out, int64_t out_stride, const bf16_t* res,
     int64_t res_stride) {
-  __shared__ BigLds sm;
+  constexpr int WAVES = BIG_WAVES;
+  constexpr int WN = WAVES / 2;              // waves along the weight rows
+  constexpr int NT = BT / WN / 16;           // MFMA tiles per wave along the weight rows
+  constexpr int HALF = NT * 8;               // SwiGLU: gate rows per wave
+  constexpr int ROWS = BT / WAVES;           // LDS rows of each tile a wave loads per stage
+  constexpr int BLK = ROWS / 16;             // ... as 1 KiB blocks of 16 rows
+  constexpr int PER = 2 * BLK;               // loads per wave per stage
+  // [stage buffer][weights, activations][row * 4 + position]: row r's 64 bytes hold its four
+  // 16-byte K units, unit u at position u ^ ((r / 2) % 4), so that the 8 lanes of a fragment
+  // read (rows c .. c + 7, one unit each) cover all 128 bytes of the banks
+  __shared__ uint4 sm[BIG_NBUF][2][BT * 4];
   const int total = gridDim.x, h = blockIdx.x;
   const int xq = total >> 3, xr = total & 7, xcd = h & 7, slot = h >> 3;
   const int L = xcd < xr ? xcd * (xq + 1) + slot : xr * (xq + 1) + (xcd - xr) * xq + slot;
@@ -546,84 +584,96 @@ __global__ __launch_bounds__(512, 1) void gemm_big_kernel(
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int c = lane & 15, q = lane >> 4;
-  const int wn = wave & 3, wm = wave >> 2;
+  const int wn = wave % WN, wm = wave / WN;
   const int64_t m0 = (int64_t)mb * BT;
-  const int ksteps = K / TK;
-  // staging: thread tid moves unit tid % 8 of LDS rows tid / 8 + 64 i (i < 4) of both tiles
-  const int r0 = tid >> 3, unit0 = tid & 7;
-  const int64_t kq = K / 8;                  // uint4 per row
-  const uint4* W4 = reinterpret_cast<const uint4*>(W);
-  const uint4* X4 = reinterpret_cast<const uint4*>(X);
-  // weight row of LDS row r0 + 64 i: plain nb*256 + r; SwiGLU: LDS rows [64 j, 64 j + 32) are
-  // the gate rows of outputs nb*128 + 32 j .., the next 32 the up rows (+ N) of the same outputs
-  auto wrow = [&](int i) -> int64_t {
-    if constexpr (EPI == EPI_SWIGLU) {       // LDS row r = r0 + 64 i: j = r / 64 = i, up = r0 >= 32
-      return (int64_t)nb * 128 + 32 * i + (r0 & 31) + (r0 >= 32 ? N : 0);
+  const int ksteps = K / BK;
+  // weight row of LDS row r: plain nb*256 + r; SwiGLU: LDS rows [2 HALF j, 2 HALF j + HALF) are
+  // the gate rows of outputs nb*128 + HALF j .., the next HALF the up rows (+ N) of the same outputs
+  auto wrow = [&](int r) -> int64_t {
+    if constexpr (EPI == EPI_SWIGLU) {
+      return (int64_t)nb * 128 + HALF * (r / (2 * HALF)) + (r % HALF) + (((r / HALF) & 1) ? N : 0);
     } else {
-      return (int64_t)nb * BT + r0 + 64 * i;
+      return (int64_t)nb * BT + r;
     }
   };
-  auto xrow = [&](int i) -> int64_t {
-    const int64_t m = m0 + r0 + 64 * i;
+  auto xrow = [&](int r) -> int64_t {
+    const int64_t m = m0 + r;
     return m < M ? m : M - 1;
   };
-  // 32-bit uint4 offsets (every operand here is < 2^32 16-byte units)
-  uint32_t wof[4], xof[4];
+  // loads: wave v fills LDS rows ROWS v .. of both tiles as BLK 1 KiB blocks of 16 rows; lane l
+  // of a block writes position l % 4 of row l / 4, i.e. K unit (l % 4) ^ ((row / 2) % 4)
+  const int unit = (lane & 3) ^ ((lane >> 3) & 3);
+  uint32_t wof[BLK], xof[BLK];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    wof[i] = (uint32_t)(wrow(i) * kq + unit0);
-    xof[i] = (uint32_t)(xrow(i) * (x_stride / 8) + unit0);
+  for (int j = 0; j < BLK; ++j) {
+    const int r = ROWS * wave + 16 * j + (lane >> 2);
+    wof[j] = (uint32_t)(wrow(r) * K * 2 + unit * 16);
+    xof[j] = (uint32_t)(xrow(r) * x_stride * 2 + unit * 16);
   }
-  const int lofs = r0 * 8 + (unit0 ^ (r0 & 7));  // + 512 i: rows + 64 i (same swizzle)
-  BigStage st[1];
-  auto load = [&](int r, int ks) {
-    const uint32_t kk = (uint32_t)(ks < ksteps ? ks : ksteps - 1) * 8u;
+  const uint32_t lbase = __builtin_amdgcn_readfirstlane(lds_u32(&sm[0][0][0])) + wave * ROWS * 64;
+  auto issue = [&](int ks, int buf) {
+    const char* wb = reinterpret_cast<const char*>(W) + (size_t)ks * (BK * 2);
+    const char* xb = reinterpret_cast<const char*>(X) + (size_t)ks * (BK * 2);
+    const uint32_t l = lbase + (uint32_t)buf * (2 * BT * 4 * 16);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st[r].w[i] = ld_stream(W4 + (wof[i] + kk));
+    for (int j = 0; j < BLK; ++j) dma16(wb, wof[j], l + 1024 * j);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st[r].x[i] = X4[xof[i] + kk];
-    __builtin_amdgcn_sched_barrier(0);
+    for (int j = 0; j < BLK; ++j) dma16(xb, xof[j], l + BT * 4 * 16 + 1024 * j);
   };
-  auto store = [&](int r, int buf) {
+  f32x4_t acc[NT][8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sm.w[buf][lofs + 512 * i] = st[r].w[i];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sm.x[buf][lofs + 512 * i] = st[r].x[i];
-  };
-  f32x4_t acc[4][8];
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt)
+  for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int fa = (64 * wn + c) * 8, fb = (128 * wm + c) * 8;    // fragment rows (+ 128 t)
-  auto compute = [&](int buf) {
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int u = (4 * s + q) ^ (c & 7);
-      uint4 a[4], b[8];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) a[t] = sm.w[buf][fa + 128 * t + u];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) b[t] = sm.x[buf][fb + 128 * t + u];
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-        for (int mt = 0; mt < 8; ++mt)
-          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(a[nt]), as_bf8(b[mt]),
-                                                                acc[nt][mt], 0, 0, 0);
-    }
+  const int u = q ^ ((c >> 1) & 3);
+  const int fa = (NT * 16 * wn + c) * 4 + u, fb = (128 * wm + c) * 4 + u;  // + 64 t: rows + 16 t
+  // fragments of one stage: NT weight tiles, 8 activation tiles (one 16-byte unit per lane each)
+  struct Frag {
+    uint4 a[NT], b[8];
   };
-  // stage s in LDS buffer s & 1 while stage s + 1's loads are in flight (two stages in flight
-  // measured slower: 256 VGPRs with spills, prefill 0.422 -> 0.458 s)
-  load(0, 0);
-  store(0, 0);
+  auto read = [&](Frag& f, int buf) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) f.a[t] = sm[buf][0][fa + 64 * t];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) f.b[t] = sm[buf][1][fb + 64 * t];
+  };
+  auto mma = [&](const Frag& f) {
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(f.a[nt]), as_bf8(f.b[mt]),
+                                                              acc[nt][mt], 0, 0, 0);
+  };
+  // Stage s lives in buffer s % BIG_NBUF.  Step ks contracts stage ks from registers while the
+  // fragments of stage ks + 1 are read: at its top this wave's loads of stage ks + 1 have landed
+  // once at most min(BIG_NBUF - 2, stages after it) stages of its loads are outstanding, and after
+  // the barrier every wave's have, and every wave has read stage ks out of its buffer, which then
+  // takes stage ks + BIG_NBUF.
+  const int nb_ = BIG_NBUF;
+#pragma unroll
+  for (int s = 0; s < BIG_NBUF; ++s)
+    if (s < ksteps) issue(s, s);
+  Frag f0, f1;
+  wait_stages<PER, BIG_NBUF - 1>(ksteps - 1);
   lds_barrier();
-  for (int ks = 0; ks < ksteps; ++ks) {
-    const bool more = ks + 1 < ksteps;       // uniform
-    if (more) load(0, ks + 1);
-    compute(ks & 1);
-    if (more) store(0, (ks + 1) & 1);
+  read(f0, 0);
+  // every step has the barrier and the reads (the last step's reads fetch a stage buffer that
+  // is never contracted): the MFMAs of a step then follow a barrier on every path, so the
+  // compiler knows that the current fragments have arrived and waits only for them
+  auto step = [&](int ks, Frag& cur, Frag& nxt) {
+    const int buf = ks % nb_;
+    wait_stages<PER, BIG_NBUF - 2>(ksteps - 2 - ks);
     lds_barrier();
+    if (ks + BIG_NBUF < ksteps) issue(ks + BIG_NBUF, buf);
+    read(nxt, buf + 1 < BIG_NBUF ? buf + 1 : 0);
+    __builtin_amdgcn_sched_barrier(0);       // the reads go out ahead of the MFMAs
+    mma(cur);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (int ks = 0; ks < ksteps; ks += 2) {
+    step(ks, f0, f1);
+    if (ks + 1 < ksteps) step(ks + 1, f1, f0);
   }
 
   // epilogue: lane (c, q) of acc[nt][mt] holds weight rows 4 q + r of tile nt = output columns
@@ -634,17 +684,18 @@ __global__ __launch_bounds__(512, 1) void gemm_big_kernel(
     if (m >= M) continue;
     if constexpr (EPI == EPI_SWIGLU) {
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int64_t n = (int64_t)nb * 128 + 32 * wn + 16 * nt + 4 * q;
+      for (int nt = 0; nt < NT / 2; ++nt) {
+        const int64_t n = (int64_t)nb * 128 + HALF * wn + 16 * nt + 4 * q;
         float y[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) y[r] = rbf(silu_f(rbf(acc[nt][mt][r]))) * rbf(acc[nt + 2][mt][r]);
+        for (int r = 0; r < 4; ++r)
+          y[r] = rbf(silu_f(rbf(acc[nt][mt][r]))) * rbf(acc[nt + NT / 2][mt][r]);
         *reinterpret_cast<uint2*>(out + m * out_stride + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
       }
     } else {
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const int64_t n = (int64_t)nb * BT + 64 * wn + 16 * nt + 4 * q;
+      for (int nt = 0; nt < NT; ++nt) {
+        const int64_t n = (int64_t)nb * BT + NT * 16 * wn + 16 * nt + 4 * q;
         float y[4];
         if constexpr (EPI == EPI_RES) {
           const uint2 rv = *reinterpret_cast<const uint2*>(res + m * res_stride + n);
@@ -742,9 +793,10 @@ int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w
                          float* pval, int32_t* pidx, float* logits, float* part,
                          int64_t part_floats, hipStream_t s) {
   if (epi != EPI_ARGMAX && ((QD_BIG_EPIS >> epi) & 1) && M >= QD_BIG_MIN_M &&
-      (epi == EPI_SWIGLU ? N % 128 == 0 : N % BT == 0)) {
+      (epi == EPI_SWIGLU ? N % 128 == 0 : N % BT == 0) &&
+      (epi == EPI_SWIGLU ? 2 * N : N) * K * 2 < (1ll << 32) && M * xs * 2 < (1ll << 32)) {
     const int64_t mbl = (M + BT - 1) / BT, nbl = epi == EPI_SWIGLU ? N / 128 : N / BT;
-    const dim3 g((unsigned)(mbl * nbl)), b(512);
+    const dim3 g((unsigned)(mbl * nbl)), b(BIG_WAVES * 64);
 #define QD_BIG(E) \
   gemm_big_kernel<E><<<g, b, 0, s>>>(x, xs, (int)M, w, (int)N, (int)K, (int)mbl, (int)nbl, out, os, res, rs)
     if (epi == EPI_RES) QD_BIG(EPI_RES);
