@@ -21,7 +21,7 @@
 // everything it read): a launch writes the copy of its parity, each word once, and zeroes the
 // other copy for the next launch, every workgroup its share, layer by layer.  Against a word of
 // {payload, 32-bit tag}, consumers load half the bytes.
-// Waits are bounded: after MG_SPIN_LIMIT polls, or once any wait has failed, a wait sets the
+// Waits are bounded: after HW_SPIN_LIMIT polls, or once any wait has failed, a wait sets the
 // error word and returns; the launch then completes with garbage instead of hanging, and the
 // host reads the error word (qd_mega_ctl_offset) after the first replay.  The workspace starts
 // zero-filled, and must be zero-filled again before a launch with another split plan (another
@@ -38,12 +38,12 @@
 #include "qd_launch.h"
 
 #include "attn_core.h"
+#include "handoff.h"
 
 namespace {
 
 constexpr int MG_NW = 8;                 // waves per workgroup
 constexpr int MG_NT = MG_NW * 64;
-constexpr uint32_t MG_SPIN_LIMIT = 1u << 20;   // polls per wait (~1 s) before giving up
 
 // model shape of this kernel (Qwen3-4B); the host checks the weights against it
 constexpr int H = 2560, INTER = 9728, HQ = 32, HKV = 8, HD = 128;
@@ -83,60 +83,9 @@ struct MegaParams {
   float eps;
 };
 
-// ------------------------------------------------------------------ hand-off words
-__device__ __forceinline__ uint32_t hw_enc(uint32_t payload) {
-  return ~(payload == 0xFFFFFFFFu ? 0xFFFFFFFEu : payload);
-}
-__device__ __forceinline__ void hw_put(uint32_t* p, uint32_t payload) {
-  __hip_atomic_store(p, hw_enc(payload), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// two words in one store (p 8-byte aligned)
-__device__ __forceinline__ void hw_put2(uint32_t* p, uint32_t lo, uint32_t hi) {
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), ((uint64_t)hw_enc(hi) << 32) | hw_enc(lo),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool hw_ready(uint32_t v) { return v != 0u; }
-__device__ __forceinline__ bool hw_ready(uint64_t v) {
-  return (uint32_t)v != 0u && (uint32_t)(v >> 32) != 0u;
-}
-// one word (uint32_t) or two (uint64_t, 8-byte aligned), as stored
-template <typename T>
-__device__ __forceinline__ T hw_raw(const T* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Slow path of a wait: poll until every word is written; bounded, and a failed wait anywhere
-// makes every later wait give up within 64 polls.
-template <typename T>
-__device__ __noinline__ T hw_spin(const T* p, uint32_t* err) {
-  T v = hw_raw(p);
-  for (uint32_t it = 1; !hw_ready(v); ++it) {
-    if ((it & 63) == 0) {
-      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-      if (it >= MG_SPIN_LIMIT) {
-        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-    }
-    __builtin_amdgcn_s_sleep(1);
-    v = hw_raw(p);
-  }
-  return v;
-}
-
-// the payload(s) of v, loaded from p, once written
-template <typename T>
-__device__ __forceinline__ T hw_wait(T v, const T* p, uint32_t* err) {
-  if (!hw_ready(v)) v = hw_spin(p, err);
-  return ~v;
-}
-
-// zero this workgroup's share of words [0, n) (n even, dst 8-byte aligned)
+// zero this workgroup's share of words [0, n)
 __device__ __forceinline__ void hw_clear(uint32_t* dst, int64_t n, int wg, int P) {
-  const int64_t a = (n / 2) * wg / P, b = (n / 2) * (wg + 1) / P;
-  uint64_t* d = reinterpret_cast<uint64_t*>(dst);
-  for (int64_t i = a + threadIdx.x; i < b; i += MG_NT)
-    __hip_atomic_store(d + i, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  ::hw_clear<MG_NT>(dst, n, wg, P);
 }
 
 // words [0, n) of src -> dst (LDS); n even, src 8-byte aligned, n / 2 <= WPT * MG_NT; two words
