@@ -50,6 +50,9 @@ constexpr int BIG_GROUP_M = QD_BIG_GROUP_M;
 #ifndef QD_BIG_MIN_M
 #define QD_BIG_MIN_M 1024
 #endif
+#ifndef QD_TILE_ROWS
+#define QD_TILE_ROWS 1     // all-rows kernel at 65..256 rows
+#endif
 #ifndef QD_BIG_EPIS
 #define QD_BIG_EPIS 7     // epilogues (bit EPI_NONE, EPI_RES, EPI_SWIGLU) that take the big tile
 #endif
@@ -713,6 +716,150 @@ __global__ __launch_bounds__(BIG_WAVES * 64, 1) void gemm_big_kernel(
   }
 }
 
+// ------------------------------------------------------------------ all rows per workgroup (65..256)
+// At a few hundred activation rows (a tree-verification forward: B x T = 256) the 128 x 128 tiles
+// give 304 gate/up workgroups for 256 CUs (48 CUs run two) and read every weight byte once per
+// 128 rows.  Here a workgroup owns a block of weight rows for all of the (<= 256) activation rows:
+// the blocks are the skinny GEMM's plan (skinny_rows: one round of workgroups) and the K splits
+// the tiled kernel's (gemm_tile_splits, the same K ranges), so the sums -- and the bits -- are the
+// tiled kernel's.  8 waves, wave w the 32 activation rows 32 w .. (2 x NT MFMA tiles; SwiGLU:
+// NT gate tiles and the NT up tiles of the same outputs); K in stages of 64 that go from global
+// memory straight into LDS (128-byte rows, unit u at u ^ (row & 7); the weight rows shared by
+// the waves), RW_NBUF stage buffers, RW_NBUF - 1 stages in flight, one barrier per stage.
+// Measured on a config-5 verify (256 rows): gate/up 58.6 -> 47.3 us, qkv 22.7 -> 20.3 us, o /
+// down unchanged; stages of 32 in 7-8 buffers (twice the bytes in flight, twice the barriers)
+// were slower (8.16 against 7.19 ms per verify).
+constexpr int RW_MAXM = 256;                // activation rows per workgroup (8 waves x 32)
+constexpr int RW_NBUF = 3;
+
+template <int EPI, bool SPLIT, int NT>
+__global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
+    const bf16_t* __restrict__ X, int64_t x_stride, int M, const bf16_t* __restrict__ W, int N,
+    int K, int rows_per_wg, int S, int ks_per, bf16_t* out, int64_t out_stride, const bf16_t* res,
+    int64_t res_stride, float* part) {
+  constexpr bool SW = EPI == EPI_SWIGLU;
+  constexpr int WT = SW ? 2 * NT : NT;       // weight tiles (gate tiles, then up tiles)
+  constexpr int WR = 16 * WT;                // staged weight rows
+  constexpr int ROWS = WR + RW_MAXM;         // staged rows per stage (weights, then activations)
+  constexpr int NBLK = ROWS / 8;             // 1 KiB load blocks per stage (8 rows x 128 bytes)
+  constexpr int PER = (NBLK + 7) / 8;        // loads per wave per stage (the last wraps around)
+  __shared__ uint4 sm[RW_NBUF][ROWS * 8];
+  const int g = blockIdx.x;
+  const int rb = g / S, split = g - rb * S;
+  const int n0 = rb * rows_per_wg;
+  const int nrows = min(rows_per_wg, N - n0);
+  const int ksteps = K / TK;
+  const int kbeg = split * ks_per, kend = min(ksteps, kbeg + ks_per);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: load bases in SGPRs
+  const int c = lane & 15, q = lane >> 4;
+  // LDS row r < WR: weight row n0 + r (SwiGLU: gate rows, then up rows + N); r >= WR: activation
+  // row r - WR; rows past the block / past M reload a valid row (never stored)
+  auto grow_off = [&](int r) -> uint32_t {
+    if (r < WR) {
+      int wr = SW ? (r % (16 * NT)) : r;
+      wr = min(wr, nrows - 1);
+      const int64_t row = (int64_t)n0 + wr + ((SW && r >= 16 * NT) ? N : 0);
+      return (uint32_t)(row * K * 2);
+    }
+    const int xm = min(r - WR, M - 1);
+    return (uint32_t)((int64_t)xm * x_stride * 2);
+  };
+  // wave w loads blocks w, w + 8, ... (mod NBLK); lane l of a block: row l / 8, position l % 8,
+  // K unit (l % 8) ^ (row % 8)
+  uint32_t voff[PER];
+  int blk[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    blk[j] = (wave + 8 * j) % NBLK;
+    const int r = blk[j] * 8 + (lane >> 3);
+    voff[j] = grow_off(r) + (uint32_t)(((lane & 7) ^ ((lane >> 3) & 7)) * 16);
+  }
+  const uint32_t lbase = __builtin_amdgcn_readfirstlane(lds_u32(&sm[0][0]));
+  auto issue = [&](int ks, int buf) {
+    const char* wb = reinterpret_cast<const char*>(W) + (size_t)ks * (TK * 2);
+    const char* xb = reinterpret_cast<const char*>(X) + (size_t)ks * (TK * 2);
+    const uint32_t l = lbase + (uint32_t)buf * (ROWS * 128);
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      dma16(blk[j] * 8 < WR ? wb : xb, voff[j], l + (uint32_t)blk[j] * 1024);
+  };
+  f32x4_t acc[WT][2];
+#pragma unroll
+  for (int t = 0; t < WT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) acc[t][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const bool active = 32 * wave < M;         // uniform per wave
+  auto compute = [&](int buf) {
+    const uint4* b0 = sm[buf];
+#pragma unroll
+    for (int s_ = 0; s_ < 2; ++s_) {
+      const int u_ = (4 * s_ + q) ^ (c & 7);
+      uint4 a_[WT], b_[2];
+#pragma unroll
+      for (int t = 0; t < WT; ++t) a_[t] = b0[(16 * t + c) * 8 + u_];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) b_[mt] = b0[(WR + 32 * wave + 16 * mt + c) * 8 + u_];
+#pragma unroll
+      for (int t = 0; t < WT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+          acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(a_[t]), as_bf8(b_[mt]),
+                                                               acc[t][mt], 0, 0, 0);
+    }
+  };
+  // stage kbeg + i in buffer i % RW_NBUF; at the top of step i this wave's loads of stage i have
+  // landed once at most min(RW_NBUF - 2, stages after it) stages of its loads are outstanding;
+  // after the barrier every wave's have, and every wave is done with stage i - 1, whose buffer
+  // then takes stage i + RW_NBUF - 1
+  constexpr int P = RW_NBUF - 1;
+  const int nst = kend - kbeg;
+#pragma unroll
+  for (int i = 0; i < P; ++i)
+    if (i < nst) issue(kbeg + i, i);
+  int buf = 0;
+  for (int i = 0; i < nst; ++i) {
+    wait_stages<PER, P - 1>(nst - 1 - i);
+    lds_barrier();
+    if (i + P < nst) issue(kbeg + i + P, buf + P < RW_NBUF ? buf + P : buf + P - RW_NBUF);
+    if (active) compute(buf);
+    buf = buf + 1 < RW_NBUF ? buf + 1 : 0;
+  }
+
+  // epilogue: lane (c, q) of acc[t][mt] holds weight rows 4 q + r of tile t = output columns
+  // n .. n + 3 of activation row m = 32 wave + 16 mt + c
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int64_t m = 32 * wave + 16 * mt + c;
+    if (m >= M) continue;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int u = 16 * t + 4 * q;          // output column offset in the block
+      if (u >= nrows) continue;
+      const int64_t n = (int64_t)n0 + u;
+      if constexpr (SPLIT) {
+        *reinterpret_cast<f32x4_t*>(part + ((int64_t)split * M + m) * N + n) = acc[t][mt];
+      } else {
+        float y[4];
+        if constexpr (SW) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[r] = rbf(silu_f(rbf(acc[t][mt][r]))) * rbf(acc[NT + t][mt][r]);
+        } else if constexpr (EPI == EPI_RES) {
+          const uint2 rv = *reinterpret_cast<const uint2*>(res + m * res_stride + n);
+          y[0] = bflo(rv.x) + rbf(acc[t][mt][0]);
+          y[1] = bfhi(rv.x) + rbf(acc[t][mt][1]);
+          y[2] = bflo(rv.y) + rbf(acc[t][mt][2]);
+          y[3] = bfhi(rv.y) + rbf(acc[t][mt][3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[r] = acc[t][mt][r];
+        }
+        *reinterpret_cast<uint2*>(out + m * out_stride + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+      }
+    }
+  }
+}
+
 int64_t tile_nblocks(int64_t N, int epi) { return epi == EPI_SWIGLU ? N / 64 : N / TN; }
 
 }  // namespace
@@ -758,6 +905,36 @@ int gemm_tile_splits(int64_t M, int64_t N, int64_t K, int epi) {
   return sp < 1 ? 1 : (int)sp;
 }
 
+// The all-rows kernel's plan for M <= 256 rows: blocks of `rows` output rows (the skinny
+// GEMM's rule for this split count), taken when a block is at most 4 MFMA tiles (SwiGLU: 3
+// gate + 3 up) and the blocks fit one round of workgroups.
+static bool rows_plan(int64_t M, int64_t N, int64_t K, int epi, int splits, int& rows, int& nt) {
+  if (!QD_TILE_ROWS || M > RW_MAXM || epi == EPI_ARGMAX) return false;
+  rows = (int)skinny_rows(N, splits);
+  nt = (rows + 15) / 16;
+  if (rows <= 0 || nt > (epi == EPI_SWIGLU ? 3 : 4)) return false;
+  if ((N + rows - 1) / rows * splits > tile_cus()) return false;
+  return (epi == EPI_SWIGLU ? 2 * N : N) * K * 2 < (1ll << 32);
+}
+
+template <int EPI, bool SPLIT>
+static void launch_rows(int nt, const bf16_t* x, int64_t xs, int M, const bf16_t* w, int N, int K,
+                        int rows, int splits, int ks_per, bf16_t* out, int64_t os,
+                        const bf16_t* res, int64_t rs, float* part, hipStream_t s) {
+  const dim3 g((unsigned)((N + rows - 1) / rows * splits)), b(512);
+#define QD_RW(NT) \
+  gemm_rows_kernel<EPI, SPLIT, NT><<<g, b, 0, s>>>(x, xs, M, w, N, K, rows, splits, ks_per, out, os, res, rs, part)
+  switch (nt) {
+    case 1: QD_RW(1); break;
+    case 2: QD_RW(2); break;
+    case 3: QD_RW(3); break;
+    default:
+      if constexpr (EPI != EPI_SWIGLU) QD_RW(4);
+      break;
+  }
+#undef QD_RW
+}
+
 int64_t gemm_tile_ws_floats(int64_t M, int64_t N, int64_t K, int epi) {
   const int sp = gemm_tile_splits(M, N, K, epi);
   return sp > 1 ? (int64_t)sp * M * N : 0;
@@ -776,7 +953,11 @@ int gemm_tile_partials(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, 
   const int ks_per = (ksteps + splits - 1) / splits;
   splits = (ksteps + ks_per - 1) / ks_per;              // no empty split
   const int64_t mblocks = (M + TM - 1) / TM, nblocks = tile_nblocks(N, EPI_NONE);
-  if (QD_TILE8)
+  int rw_rows = 0, rw_nt = 0;
+  if (rows_plan(M, N, K, EPI_NONE, splits, rw_rows, rw_nt))
+    launch_rows<EPI_NONE, true>(rw_nt, x, xs, (int)M, w, (int)N, (int)K, rw_rows, splits, ks_per,
+                                nullptr, 0, nullptr, 0, part, s);
+  else if (QD_TILE8)
     gemm_tile8_kernel<EPI_NONE, true><<<dim3((unsigned)(mblocks * nblocks * splits)), dim3(512), 0, s>>>(
         x, xs, (int)M, w, (int)N, (int)K, (int)mblocks, (int)nblocks, ks_per, nullptr, 0, nullptr,
         0, part);
@@ -813,9 +994,14 @@ int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w
   splits = (ksteps + ks_per - 1) / ks_per;              // no empty split
   const dim3 grid((unsigned)(mblocks * nblocks * splits)), block(256);
   const int Mi = (int)M, Ni = (int)N, Ki = (int)K, mbi = (int)mblocks, nbi = (int)nblocks;
+  int rw_rows = 0, rw_nt = 0;
+  const bool rw = rows_plan(M, N, K, epi, splits, rw_rows, rw_nt);
 #define QD_TILE(E, SP)                                                                           \
   do {                                                                                           \
-    if (QD_TILE8 && E != EPI_ARGMAX)                                                             \
+    if (rw && E != EPI_ARGMAX)                                                                   \
+      launch_rows<E == EPI_ARGMAX ? EPI_NONE : E, SP>(rw_nt, x, xs, Mi, w, Ni, Ki, rw_rows,      \
+                                                      splits, ks_per, out, os, res, rs, part, s); \
+    else if (QD_TILE8 && E != EPI_ARGMAX)                                                        \
       gemm_tile8_kernel<E == EPI_ARGMAX ? EPI_NONE : E, SP><<<grid, dim3(512), 0, s>>>(          \
           x, xs, Mi, w, Ni, Ki, mbi, nbi, ks_per, out, os, res, rs, part);                       \
     else                                                                                         \

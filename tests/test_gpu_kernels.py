@@ -141,7 +141,7 @@ SHAPES = {"qkv": (6144, 2560), "o": (2560, 4096), "gu": (9728, 2560), "down": (2
 # summed by a second kernel where the tile grid is small: qkv / o / down at 100 and 256 rows,
 # o / down at 600); 1040 rows: the 256 x 256-tile prefill kernel (four full row blocks and a
 # ragged 16-row one)
-@pytest.mark.parametrize("B", [1, 2, 3, 16, 20, 32, 64, 100, 256, 600, 1040])
+@pytest.mark.parametrize("B", [1, 2, 3, 16, 20, 32, 64, 65, 100, 200, 256, 600, 1040])
 @pytest.mark.parametrize("name", ["qkv", "o", "gu", "down"])
 def test_linear_epilogues(ops, name, B):
     say(f"linear {name} B={B}")
