@@ -33,6 +33,7 @@
 
 #include "attn_mfma.h"
 #include "handoff.h"
+#include "norm_row.h"
 #include "skinny_core.h"
 
 namespace {
@@ -44,7 +45,6 @@ constexpr int NQKV = (HQ + 2 * HKV) * HD;   // 6144
 constexpr int QD = HQ * HD;                 // 4096
 constexpr int SQ = 2, SO = 4, SD = 4;       // K splits of qkv, o and down, as qd_decode_step's
 constexpr int MIN_WG = 256;                 // workgroups: >= every phase's block count
-constexpr int NCH = H / 8;                  // 16-byte chunks of a row
 
 // GEMM phases: 32-row tiles (MT 2) of 3 16-row weight tiles (NT 3): the plans at 256 CUs
 constexpr int D_NONE = skinny_depth<2, 3, EPI_NONE>();
@@ -91,128 +91,6 @@ union MbSmem {
 static_assert(SkinnyShape<2, 3, EPI_NONE>::LDS_U4 <= SkinnyShape<2, 3, EPI_SWIGLU>::LDS_U4,
               "LDS of the plain GEMM phases");
 
-// RMSNorm of row `row` by threads 0..255 (every thread of the workgroup reaches the barriers).
-// S > 0: acc = the S split partials part[S][B][H] (hand-off words) summed in split order,
-// r' = bf16(res + bf16(acc)) written back to res -- part_add_rmsnorm_kernel<S>; S == 0: r' = res
-// (add_rmsnorm_kernel without an addend).  y = bf16(bf16(r' * rstd) * w) as hand-off words
-// (HWOUT) or plain bf16 rows.
-template <int S, bool HWOUT>
-__device__ void mb_norm_row(const uint32_t* part, int B, int row, bf16_t* res,
-                            const bf16_t* __restrict__ w, void* y, float eps, float* red,
-                            uint32_t* err) {
-  constexpr int J = (NCH + 255) / 256;         // chunks per thread (2: c = tid, tid + 256)
-  const int tid = threadIdx.x;
-  uint4* rr = reinterpret_cast<uint4*>(res + (int64_t)row * H);
-  const uint4* wr = reinterpret_cast<const uint4*>(w);
-  float ss = 0.f;
-  uint4 rv[J], gv[J];
-  if (tid < 256) {
-    if constexpr (S > 0) {
-      // every split's words of both chunks are requested at once, and re-requested together
-      // until all have arrived (one round trip per poll, not one per word)
-      const uint64_t* base = reinterpret_cast<const uint64_t*>(part + (int64_t)row * H);
-      const int64_t split_stride = (int64_t)B * H / 2;        // uint64 pairs per split
-      uint64_t raw[J][S][4];
-      auto fetch = [&]() {
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-          const int c = tid + 256 * j;
-#pragma unroll
-          for (int s = 0; s < S; ++s)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              raw[j][s][e] = c < NCH ? hw_raw(base + s * split_stride + 4 * c + e) : ~0ull;
-        }
-      };
-      auto ready = [&]() {
-        bool ok = true;
-#pragma unroll
-        for (int j = 0; j < J; ++j)
-#pragma unroll
-          for (int s = 0; s < S; ++s)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ok = ok && hw_ready(raw[j][s][e]);
-        return ok;
-      };
-      fetch();
-      if (!ready()) {
-        for (uint32_t it = 1; !ready(); ++it) {
-          if ((it & 63) == 0) {
-            if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-            if (it >= HW_SPIN_LIMIT) {
-              __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              break;
-            }
-          }
-          __builtin_amdgcn_s_sleep(1);
-          fetch();
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const int c = tid + 256 * j;
-        if (c < NCH) {
-          float a[8];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint64_t v = ~raw[j][0][e];
-            a[2 * e] = __uint_as_float((uint32_t)v);
-            a[2 * e + 1] = __uint_as_float((uint32_t)(v >> 32));
-          }
-#pragma unroll
-          for (int s = 1; s < S; ++s)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const uint64_t v = ~raw[j][s][e];
-              a[2 * e] += __uint_as_float((uint32_t)v);
-              a[2 * e + 1] += __uint_as_float((uint32_t)(v >> 32));
-            }
-          const uint4 r = rr[c];
-          uint4 o;
-          o.x = pack2(bflo(r.x) + rbf(a[0]), bfhi(r.x) + rbf(a[1]));
-          o.y = pack2(bflo(r.y) + rbf(a[2]), bfhi(r.y) + rbf(a[3]));
-          o.z = pack2(bflo(r.z) + rbf(a[4]), bfhi(r.z) + rbf(a[5]));
-          o.w = pack2(bflo(r.w) + rbf(a[6]), bfhi(r.w) + rbf(a[7]));
-          rv[j] = o;
-          gv[j] = wr[c];
-          ss += sumsq8(o);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const int c = tid + 256 * j;
-        if (c < NCH) {
-          rv[j] = rr[c];
-          gv[j] = wr[c];
-          ss += sumsq8(rv[j]);
-        }
-      }
-    }
-  }
-  // the 256 threads' sum as block_sum256: wave sums, then waves 0..3 in order
-  ss = wave_sum(ss);
-  if (tid < 256 && (tid & 63) == 0) red[tid >> 6] = ss;
-  lds_barrier();
-  const float rstd = rstd_of(red[0] + red[1] + red[2] + red[3], H, eps);
-  if (tid < 256) {
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int c = tid + 256 * j;
-      if (c < NCH) {
-        const uint4 o = norm8(rv[j], gv[j], rstd);
-        if constexpr (HWOUT) {
-          hw_put4(static_cast<uint32_t*>(y) + (int64_t)row * (H / 2) + 4 * c, o.x, o.y, o.z, o.w);
-        } else {
-          reinterpret_cast<uint4*>(static_cast<bf16_t*>(y) + (int64_t)row * H)[c] = o;
-        }
-        if constexpr (S > 0) rr[c] = rv[j];
-      }
-    }
-  }
-  lds_barrier();                                // red is free again
-}
-
 __global__ __launch_bounds__(MB_NT, 1) void mega_batch_kernel(MbParams p) {
   __shared__ MbSmem sm;
   const int wg = blockIdx.x, P = gridDim.x, B = p.B;
@@ -234,9 +112,9 @@ __global__ __launch_bounds__(MB_NT, 1) void mega_batch_kernel(MbParams p) {
     // x' = x + the previous layer's down partials; xn1 = RMSNorm(x'; ln1)
     if (wg < B) {
       if (l == 0)
-        mb_norm_row<0, true>(nullptr, B, wg, p.x, p.ln1, LL + ly.xn1, p.eps, sm.red, err);
+        norm_row<0, true, H>(nullptr, B, wg, p.x, p.ln1, LL + ly.xn1, p.eps, sm.red, err);
       else
-        mb_norm_row<SD, true>(LL - ly.per_layer + ly.dp, B, wg, p.x, p.ln1 + (int64_t)l * H,
+        norm_row<SD, true, H>(LL - ly.per_layer + ly.dp, B, wg, p.x, p.ln1 + (int64_t)l * H,
                               LL + ly.xn1, p.eps, sm.red, err);
     }
     // qkv partials
@@ -263,7 +141,7 @@ __global__ __launch_bounds__(MB_NT, 1) void mega_batch_kernel(MbParams p) {
     lds_barrier();
     // x'' = x' + o partials; xn2 = RMSNorm(x''; ln2)
     if (wg < B)
-      mb_norm_row<SO, true>(LL + ly.op, B, wg, p.x, p.ln2 + (int64_t)l * H, LL + ly.xn2, p.eps,
+      norm_row<SO, true, H>(LL + ly.op, B, wg, p.x, p.ln2 + (int64_t)l * H, LL + ly.xn2, p.eps,
                             sm.red, err);
     // act = SwiGLU(xn2 . Wgate^T, xn2 . Wup^T)
     if (wg < p.blk_gu)
@@ -283,7 +161,7 @@ __global__ __launch_bounds__(MB_NT, 1) void mega_batch_kernel(MbParams p) {
   }
   // final RMSNorm of x + the last down partials, for the LM head launch
   if (wg < B)
-    mb_norm_row<SD, false>(ll + (int64_t)(p.L - 1) * ly.per_layer + ly.dp, B, wg, p.x,
+    norm_row<SD, false, H>(ll + (int64_t)(p.L - 1) * ly.per_layer + ly.dp, B, wg, p.x,
                            p.final_norm, p.xn_out, p.eps, sm.red, err);
   // done words; workgroup 0 advances the epoch once every workgroup has posted its word
   uint32_t* done = ll + (int64_t)p.L * ly.per_layer;
