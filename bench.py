@@ -443,9 +443,10 @@ def layer_kernels_large(reps=20):
     return out
 
 
-def cpu_baseline(budget_s=15.0, prompt_len=32):
+def cpu_baseline(budget_s=15.0, prompt_len=512):
     """The CPU oracle (torch CPU, oneDNN bf16) on the same 36-layer architecture and
-    generator: prefill a short prompt, then time greedy decode steps for ~budget_s."""
+    generator: prefill config 3's 512-token prompt (untimed), then time greedy decode steps for
+    ~budget_s, on the host's CPU share (OMP_NUM_THREADS threads: 16 per GPU on the GPU box)."""
     import numpy as np
     import torch
     sys.path.insert(0, ROOT)
@@ -454,7 +455,12 @@ def cpu_baseline(budget_s=15.0, prompt_len=32):
     if not os.path.exists(lib):
         import subprocess
         subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
-    threads = torch.get_num_threads()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count()
     t0 = time.perf_counter()
     ref = qwen3_ref.Qwen3Ref.from_synth(1, 36)
     gen_s = time.perf_counter() - t0
@@ -479,8 +485,10 @@ def cpu_baseline(budget_s=15.0, prompt_len=32):
     return {"value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": (f"oracle/qwen3_ref.py greedy decode, 36-layer Qwen3-4B shape, B=1, "
                        f"{n} steps after a {prompt_len}-token prefill ({dt:.1f} s; weight "
-                       f"generation {gen_s:.1f} s untimed); torch {torch.__version__} CPU on "
-                       f"{threads} threads of {cpu}")}
+                       f"generation {gen_s:.1f} s and the prefill untimed); "
+                       f"torch {torch.__version__} CPU on "
+                       f"{threads} threads (the host's CPU share; {affinity} in the affinity "
+                       f"mask) of {cpu}")}
 
 
 def main():
