@@ -330,8 +330,9 @@ class BlockRunner:
 
 # Rows per causal prefill forward.  6144 = 24 blocks of the prefill GEMM's 256-row tiles, so the
 # o / down projections (10 blocks of 256 weight rows) fill 240 of the 256 CUs in one round.
-# Measured on MI355X (prefill + first token): 4 x 8192 0.422 s (4096 rows: 0.432, 8192: 0.442,
-# 16384: 0.466); 32 x 2048 0.608 s (4096: 0.660, 8192: 0.646, 16384: 0.608).
+# Measured on MI355X (prefill + first token): 4 x 8192 0.395-0.398 s (4096 rows: 0.408, 5120:
+# 0.399, 7168: 0.430, 8192: 0.418, 12288: 0.404, 16384: 0.441); 32 x 2048 0.560 s (4096: 0.614,
+# 5120: 0.564, 7168: 0.658, 8192: 0.606, 12288: 0.548, 16384: 0.565).
 PREFILL_ROWS = 6144
 
 
