@@ -1,5 +1,6 @@
 """Shared comparison helpers for the parity tests (bf16 ulp distances, margin rule)."""
 
+import json
 import os
 import subprocess
 
@@ -45,6 +46,16 @@ def assert_ulp(a, b, max_ulp, what="", abs_floor=0.0):
 # the top logit (tests/test_oracle.py: the golden ids sit up to 0.0625 below the oracle's
 # argmax), so against the oracle a "near tie" is a top-2 gap within 2 ulp at |logit| < 8.
 ORACLE_TIE = 0.0625 + 1e-6
+
+# At the benchmarks' depth (36 layers) the floor is measured, not assumed: two equally valid
+# restatements of the oracle -- softmax against the global row maximum, and the online softmax
+# over 64-key blocks that tiled kernels compute -- teacher-forced over the config-3 run disagree
+# on the argmax at 39 of 543 positions, with the second one's choice up to 0.15625 (5 bf16 ulp
+# at |logit| < 8) below the first one's argmax (tests/golden/depth_noise.json, written by
+# tests/golden/make_depth_noise.py).  A 36-layer run is held to that floor: an implementation
+# as valid as the oracle itself would fail anything tighter.
+DEPTH_NOISE = json.load(open(os.path.join(GOLDEN, "depth_noise.json")))
+DEPTH_TIE = DEPTH_NOISE["max_deficit_B_under_A"] + 1e-6
 
 
 def margin_report(tokens, ref_logits, margin=1e-2):

@@ -11,8 +11,10 @@ seeded model (seed 1) through Engine.generate / generate_tree, against the CPU o
 
 The stored runs come from tests/golden/make_depth_golden.py (the same oracle, prompts from
 synth.prompt_ids).  Token rule against a stored run (helpers.fixture_rule): identical ids, the
-first difference allowed only at an oracle near tie (top-2 gap within 2 bf16 ulp) where the
-engine picked the oracle's second choice."""
+first difference allowed only at an oracle near tie where the engine picked the oracle's second
+choice.  At this depth a near tie is a top-2 gap within helpers.DEPTH_TIE (5 bf16 ulp), the
+measured disagreement between two equally valid restatements of the oracle
+(tests/golden/depth_noise.json); the teacher-forced margin rule uses the same allowance."""
 
 import json
 import os
@@ -22,7 +24,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import GOLDEN, ORACLE_TIE, ensure_oracle_built, fixture_rule, margin_rule
+from helpers import DEPTH_TIE, GOLDEN, ensure_oracle_built, fixture_rule, margin_rule
 from oracle import qwen3_ref as R
 from oracle import synth
 
@@ -73,9 +75,9 @@ def test_config3_end_to_end(eng36, ref36):
     from qdecode import model as M
     assert eng36.shape.decode.mega == M.mega_default(eng36.model, 1)   # the benchmark's tier
     print(f"persistent step: {eng36.shape.decode.mega}; ids {toks[0].tolist()}", flush=True)
-    fixture_rule(toks[0], c["rows"][0])
+    fixture_rule(toks[0], c["rows"][0], tie=DEPTH_TIE)
     tl = _teacher(ref36, prompt[0], toks[0], "config 3")
-    assert margin_rule(toks, tl, margin=ORACLE_TIE, what="config 3, 36 layers") == []
+    assert margin_rule(toks, tl, margin=DEPTH_TIE, what="config 3, 36 layers") == []
 
 
 def test_config4_end_to_end(eng36, ref36):
@@ -85,9 +87,9 @@ def test_config4_end_to_end(eng36, ref36):
     assert toks.shape == (c["B"], c["N"])
     for rec in c["rows"]:
         print(f"row {rec['row']}: {toks[rec['row']].tolist()}", flush=True)
-        fixture_rule(toks[rec["row"]], rec)
+        fixture_rule(toks[rec["row"]], rec, tie=DEPTH_TIE)
     tl = _teacher(ref36, prompt[0], toks[0], "config 4 row 0")
-    assert margin_rule(toks[:1], tl, margin=ORACLE_TIE, what="config 4 row 0") == []
+    assert margin_rule(toks[:1], tl, margin=DEPTH_TIE, what="config 4 row 0") == []
 
 
 def test_config5_tree_and_plain_at_8192(eng36):
@@ -104,8 +106,8 @@ def test_config5_tree_and_plain_at_8192(eng36):
     assert got.shape == (c["B"], c["N"])
     for rec in c["rows"]:
         print(f"tree row {rec['row']}: {got[rec['row']].tolist()}", flush=True)
-        fixture_rule(got[rec["row"]], rec)
+        fixture_rule(got[rec["row"]], rec, tie=DEPTH_TIE)
     plain = np.array(list(eng36.generate(prompt.tolist(), c["N"]))).T
     for rec in c["rows"]:
         print(f"plain row {rec['row']}: {plain[rec['row']].tolist()}", flush=True)
-        fixture_rule(plain[rec["row"]], rec)
+        fixture_rule(plain[rec["row"]], rec, tie=DEPTH_TIE)
