@@ -156,36 +156,59 @@ constexpr int64_t BLOCK_CHUNK = 512;
 // v_mfma_f32_16x16x32_bf16.  Workgroup = (key split of `chunk` keys, KV head, block of
 // BA_TQ = 64 query tokens of one sequence), 8 waves: wave w handles query head kvh*4 + (w & 3)
 // for the block's tokens 32 (w >> 2) .. + 31 (two 16-row tiles), so every staged K/V tile
-// serves 64 tokens x 4 heads.  Keys go in tiles of 32:
+// serves 64 tokens x 4 heads.  Keys go in tiles of BA_KT = 64:
 //  * S' = K . Q^T: A = K tile rows (LDS, 16-byte units XOR-swizzled by key), B = the lane's query
 //    row (registers); lane (c, q) ends up holding the scores of its query row c against keys
-//    4q..4q+3 and 16+4q..16+4q+3 of the tile;
-//  * online softmax per query row in fp32 (the row max / sum across the four q lanes through
-//    permlane swaps), P rounded to bf16;
-//  * O^T += V^T . P^T: A = V^T fragments, B = the lane's 8 probabilities, taken in that same key
-//    order (a permutation of the contraction index shared by both operands), so O^T's lane (c, q)
-//    holds dims 16 dt + 4q..+3 of row c and the per-row rescale needs no cross-lane traffic.  V is
-//    staged key-major like K (one 16-byte store per thread) and read transposed with gfx950's
-//    ds_read_b64_tr_b16: within a 16-lane group, lane j = 4a + b receives element b of the
-//    8-byte pieces that lanes a, a + 4, a + 8, a + 12 address, so lane i addressing dims
-//    16 dt + 4 (i % 4) .. + 3 of key 4q + i / 4 makes lane c receive V[4q + r][16 dt + c],
-//    r = 0..3 (measured on MI355X with an in-bounds layout probe);
-//  * staging: thread i moves K and V unit i % 16 of key i / 16 of a tile; the next three tiles'
-//    loads are in flight (a register ring) while a tile is staged and contracted.
-// Writes (m, l, acc) partials per (query row, head, split) -- ws_acc[idx * 128 + d], ws_ml[idx * 2],
-// idx = ((b*T + t)*Hq + h)*splits + split -- which attn_merge_kernel merges.
+//    16 h + 4q .. 16 h + 4q + 3 of the tile, h = 0..3;
+//  * softmax in log2 units: s' = (q.k) * 128^-1/2 * log2(e) (the scale folded into one fma with
+//    the subtraction of the row's reference maximum m), p = 2^(s' - m) on v_exp_f32, P rounded
+//    to bf16.  m moves only when a tile's maximum exceeds it by more than BA_TAU, so p <= 2^TAU
+//    and the rescale of O and l by 2^(m_old - m_new) runs only when some row's maximum jumped
+//    (the first visible tile, rarely after); the row max / sum across the four q lanes of a row
+//    go through permlane swaps;
+//  * O^T += V^T . P^T per 32-key half: A = V^T fragments, B = the lane's 8 probabilities, taken
+//    in that same key order (a permutation of the contraction index shared by both operands), so
+//    O^T's lane (c, q) holds dims 16 dt + 4q..+3 of row c and the per-row rescale needs no
+//    cross-lane traffic.  V is staged key-major like K (one 16-byte store per thread and key) and
+//    read transposed with gfx950's ds_read_b64_tr_b16: within a 16-lane group, lane j = 4a + b
+//    receives element b of the 8-byte pieces that lanes a, a + 4, a + 8, a + 12 address, so lane
+//    i addressing dims 16 dt + 4 (i % 4) .. + 3 of key 4q + i / 4 makes lane c receive
+//    V[4q + r][16 dt + c], r = 0..3 (measured on MI355X with an in-bounds layout probe);
+//  * pipeline: three LDS tile buffers; in the step of tile i a wave contracts S' of tile i + 1
+//    (its MFMAs independent of the softmax of tile i, which the compiler interleaves with them),
+//    runs the softmax and O update of tile i, and the workgroup stages tile i + 2 from registers
+//    loaded two steps earlier (thread i moves K and V unit i % 16 of keys i / 16 and i / 16 + 32);
+//    one barrier per tile.
+// Numerics against the math path: every p is one bf16 rounding of a probability scaled by at
+// most 2^TAU, and the running rescale is exact up to fp32 rounding, as in any online softmax.
+// Writes (m, l, acc) partials per (query row, head, split) -- m in natural-log units, as
+// attn_merge_kernel expects; ws_acc[idx * 128 + d], ws_ml[idx * 2], idx = ((b*T + t)*Hq + h)*splits
+// + split -- or, with one split, the normalised bf16 rows.
 constexpr int BA_TQ = 64;
+constexpr int BA_KT = 64;
+#ifndef QD_BA_NBUF
+#define QD_BA_NBUF 4
+#endif
+constexpr int BA_NBUF = QD_BA_NBUF;   // LDS tile buffers (BA_NBUF - 3 tiles in flight beyond the next)
+#ifndef QD_BA_TAU
+#define QD_BA_TAU 8.0f
+#endif
+constexpr float BA_TAU = QD_BA_TAU;
+constexpr float BA_LN2 = 0.69314718055994531f;
 
+struct BlockAttnLds {
+  uint4 k[BA_NBUF][BA_KT * 16];
+  uint4 v[BA_NBUF][BA_KT * 16];
+};
 
 __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
     const bf16_t* __restrict__ v_cache, const int64_t* __restrict__ base_ptr,
     const uint64_t* __restrict__ anc, int64_t T, int Hq, int Hkv, int64_t cap, int64_t chunk,
-    float scale, float* ws_acc, float* ws_ml, bf16_t* __restrict__ out) {
+    float scale_log2, float* ws_acc, float* ws_ml, bf16_t* __restrict__ out) {
   typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
   typedef __attribute__((ext_vector_type(4))) float f32x4_t;
-  __shared__ uint4 ks[32 * 16];
-  __shared__ uint4 vs[32 * 16];
+  __shared__ BlockAttnLds sm;
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int splits = gridDim.x;
   const int64_t QB = (T + BA_TQ - 1) / BA_TQ;
@@ -214,161 +237,219 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
   if (kend > base + T) kend = base + T;
   if (!anc && kend > base + tb + BA_TQ) kend = base + tb + BA_TQ;   // causal: later keys unseen
   if (kend > cap) kend = cap;
-  const int ntiles = kend > start ? (int)((kend - start + 31) / 32) : 0;
+  const int ntiles = kend > start ? (int)((kend - start + BA_KT - 1) / BA_KT) : 0;
   const int64_t head_off = ((b * Hkv + kvh) * cap) * 128;
   const uint4* kb = reinterpret_cast<const uint4*>(k_cache + head_off);
   const uint4* vb = reinterpret_cast<const uint4*>(v_cache + head_off);
+  // o[rt][dt]: O^T dims 16 dt + 4 q4 .. + 3 of the lane's row c; lsum[rt]: the fp32 sum of the
+  // lane's probabilities of that row (its four q lanes hold disjoint keys)
   float m[2] = {M_FLOOR, M_FLOOR}, lsum[2] = {0.f, 0.f};
   f32x4_t o[2][8];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) o[rt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int skey = tid >> 4, su = tid & 15;
-  // load tile `it` (clamped into the cache: tiles past the range reload valid keys, unused)
-#define BA_LD(IT, KX, VX)                                                      \
-  {                                                                            \
-    const int64_t jn_ = start + 32 * (int64_t)(IT) + skey;                     \
-    const int64_t j_ = jn_ < cap ? jn_ : cap - 1;                              \
-    KX = kb[j_ * 16 + su];                                                     \
-    VX = vb[j_ * 16 + su];                                                     \
-  }
-  auto stage = [&](const uint4& kx, const uint4& vx) {
-    ks[skey * 16 + (su ^ (skey & 15))] = kx;
-    vs[skey * 16 + (su ^ (skey & 15))] = vx;
+  // Staging by DMA (global_load_lds_dwordx4, no registers): wave w moves the 1 KiB blocks 2w
+  // and 2w + 1 of a tile's K and of its V (block j = keys 4j .. 4j + 3); lane l of block j lands
+  // in LDS slot 64 j + l = unit (l & 15) of key 4 j + (l >> 4) as stored, i.e. logical unit
+  // (l & 15) ^ (key & 15) (the XOR swizzle the fragment reads undo).  Keys past the cache
+  // reload its last row (valid, never used).  Key indices and byte offsets within a head are
+  // 32-bit: cap is at most 1024 splits x BLOCK_CHUNK keys (checked by the entry points), 134 MB
+  // of K per head.
+  const int dk0 = 8 * wave + (lane >> 4), dk1 = dk0 + 4;
+  const uint32_t du0 = (uint32_t)((lane & 15) ^ (dk0 & 15)) * 16u;
+  const uint32_t du1 = (uint32_t)((lane & 15) ^ (dk1 & 15)) * 16u;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_u32(&sm.k[0][0])) + (uint32_t)wave * 2048u;
+  constexpr uint32_t TILE_B = BA_KT * 16 * 16;                  // bytes of one K (V) tile
+  constexpr uint32_t V_OFF = BA_NBUF * TILE_B;                  // sm.v after sm.k
+  const int start32 = (int)start, last = (int)cap - 1;
+  auto issue = [&](int it, int buf) {
+    const int ts = start32 + BA_KT * it;
+    const uint32_t oa = (uint32_t)min(ts + dk0, last) * 256u + du0;
+    const uint32_t ob = (uint32_t)min(ts + dk1, last) * 256u + du1;
+    const uint32_t l = lds0 + (uint32_t)buf * TILE_B;
+    dma16(kb, oa, l);
+    dma16(kb, ob, l + 1024u);
+    dma16(vb, oa, l + V_OFF);
+    dma16(vb, ob, l + V_OFF + 1024u);
   };
-  // this lane's transposed-read address for V dims 16 dt + 4 (c % 4) .. + 3 of key 16 h2 + 4 q4 +
-  // c / 4: 16-byte unit 2 dt + (c / 2) % 2, half c % 2
-  auto vt_addr = [&](int dt, int h2) -> const void* {
-    const int key = 16 * h2 + 4 * q4 + (c >> 2);
-    const int u = 2 * dt + ((c >> 1) & 1);
-    return reinterpret_cast<const char*>(&vs[key * 16 + (u ^ (key & 15))]) + 8 * (c & 1);
-  };
-  auto contract = [&](int64_t j0) {
-    // S' = K . Q^T for both key halves and both row tiles
-    f32x4_t sc[2][2];
+  // S' of the tile in `buf` for both row tiles: sc[rt][h] = keys 16 h + 4 q4 .. + 3, row c
+  auto scores = [&](int buf, f32x4_t (&sc)[2][4]) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) sc[rt][h2] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int h = 0; h < 4; ++h) sc[rt][h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-      const int key = 16 * h2 + c;
+    for (int h = 0; h < 4; ++h) {
+      const int key = 16 * h + c;                            // key & 15 == c
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const uint4 kf = ks[key * 16 + ((4 * kk + q4) ^ c)];
+        const uint4 kf = sm.k[buf][key * 16 + ((4 * kk + q4) ^ c)];
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
-          sc[rt][h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          sc[rt][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
               __builtin_bit_cast(bf16x8_t, kf), __builtin_bit_cast(bf16x8_t, qf[rt][kk]),
-              sc[rt][h2], 0, 0, 0);
+              sc[rt][h], 0, 0, 0);
       }
-    }
-    // online softmax of both row tiles; P packed in the key order {4q4..+3, 16+4q4..+3}
-    uint4 pf[2];
-    float alpha[2];
-    // a tile of cached keys only (below base and kend) is visible to every row: no per-score
-    // test (the common case: all of the context but the block's own split)
-    const bool whole = j0 + 32 <= base && j0 + 32 <= kend;   // uniform over the workgroup
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      float sv[8];
-      if (whole) {
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) sv[4 * h2 + r] = sc[rt][h2][r] * scale;
-      } else {
-        // key j = j0 + 16 h2 + 4 q4 + r, as offsets from the tile start and from base
-        const int jrel0 = (int)(j0 - base);                   // may be negative
-        const int lim = (int)(kend - j0);                     // keys of the tile below kend
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int o = 16 * h2 + 4 * q4 + r;
-            const int jb = jrel0 + o;                         // block index (< 0: cached key)
-            bool vis = o < lim;
-            if (jb >= 0)
-              vis = vis && (anc ? jb < 64 && ((mask[rt] >> (jb & 63)) & 1ull) != 0
-                                : (int64_t)jb <= tok[rt]);
-            sv[4 * h2 + r] = vis ? sc[rt][h2][r] * scale : NEG_INF;
-          }
-      }
-      float mx = sv[0];
-#pragma unroll
-      for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
-      mx = fmaxf(mx, lane_xor16(mx));
-      mx = fmaxf(mx, lane_xor32(mx));
-      const float mn = fmaxf(m[rt], mx);
-      alpha[rt] = __expf(m[rt] - mn);
-      m[rt] = mn;
-      float p[8], ps = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) { p[e] = __expf(sv[e] - mn); ps += p[e]; }
-      lsum[rt] = lsum[rt] * alpha[rt] + ps;
-      pf[rt] = make_uint4(pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7]));
-    }
-    // rescale O only if some row's running max moved (alpha == 1 exactly otherwise, and
-    // x * 1 == x: skipping it changes no bit); wave-uniform
-    if (__ballot(alpha[0] != 1.f || alpha[1] != 1.f) != 0) {
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) o[rt][dt] *= alpha[rt];
-    }
-    // O^T += V^T . P^T: V^T fragment of dims 16 dt + c, keys 4q4..+3 and 16+4q4..+3
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const uint2 lo = lds_read_tr16(vt_addr(dt, 0));
-      const uint2 hi = lds_read_tr16(vt_addr(dt, 1));
-      const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-        o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            __builtin_bit_cast(bf16x8_t, vf), __builtin_bit_cast(bf16x8_t, pf[rt]), o[rt][dt], 0,
-            0, 0);
     }
   };
-  // Tile `it` is staged from ring slot it % 3 and the slot is then refilled with tile it + 3.
-  // The loop body is three tiles with no exit between them (an exit there lets the compiler
-  // sink a refill behind the contraction it should overlap); the last 0..2 tiles follow it.
-  uint4 k0, v0, k1, v1, k2, v2;
-  BA_LD(0, k0, v0);
-  BA_LD(1, k1, v1);
-  BA_LD(2, k2, v2);
-  int it = 0;
-  for (; it + 2 < ntiles; it += 3) {
-    lds_barrier();                                     // the previous tile is consumed
-    stage(k0, v0);
-    lds_barrier();                                     // the tile is staged
-    BA_LD(it + 3, k0, v0);
-    contract(start + 32 * (int64_t)it);
+  // invisible keys of a tile that touches the block or the range end -> -inf, from one 64-bit
+  // visibility word per row (bit i = tile key j0 + i): the tile's cached keys (below base), the
+  // block keys the row sees (its ancestor bits, or for a causal chunk the keys up to itself),
+  // cut at kend
+  auto mask_tile = [&](int64_t j0, f32x4_t (&sc)[2][4]) {
+    const int jrel0 = (int)(j0 - base);                       // block index of key j0 (may be < 0)
+    const int lim = (int)(kend - j0);                         // keys of the tile below kend
+    const uint64_t limbits = lim >= 64 ? ~0ull : lim <= 0 ? 0ull : (1ull << lim) - 1;
+    const uint64_t cached = jrel0 >= 0 ? 0ull : jrel0 <= -64 ? ~0ull : (1ull << -jrel0) - 1;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      uint64_t blk;
+      if (anc) {
+        blk = jrel0 >= 64 ? 0ull : jrel0 >= 0 ? mask[rt] >> jrel0
+                                   : jrel0 <= -64 ? 0ull : mask[rt] << -jrel0;
+      } else {
+        const int64_t n = tok[rt] - jrel0 + 1;                // block keys jrel0 .. tok visible
+        blk = n <= 0 ? 0ull : n >= 64 ? ~0ull : (1ull << n) - 1;
+      }
+      const uint64_t vis = (cached | blk) & limbits;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const uint32_t nib = (uint32_t)(vis >> (16 * h + 4 * q4)) & 15u;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (!((nib >> r) & 1u)) sc[rt][h][r] = NEG_INF;
+      }
+    }
+  };
+  // softmax of a tile's scores: rescale O / l if a row's maximum jumped, then the tile's
+  // probabilities as bf16 MFMA B fragments pf (keys 8 j .. 8 j + 7 of the lane's order)
+  auto softmax = [&](const f32x4_t (&sc)[2][4], uint4 (&pf)[2][2]) {
+    float mx[2];
+    bool need[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float x[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        x[h] = fmaxf(fmaxf(sc[rt][h][0], sc[rt][h][1]), fmaxf(sc[rt][h][2], sc[rt][h][3]));
+      float y = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+      y = fmaxf(y, lane_xor16(y));
+      y = fmaxf(y, lane_xor32(y));
+      mx[rt] = y * scale_log2;                                // = max of the scaled scores
+      need[rt] = mx[rt] > m[rt] + BA_TAU;
+    }
+    if (__ballot(need[0] || need[1]) != 0) {                 // wave-uniform
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const float mn = need[rt] ? mx[rt] : m[rt];
+        const float a = __builtin_amdgcn_exp2f(m[rt] - mn);  // 1 for rows that keep m
+        m[rt] = mn;
+        lsum[rt] *= a;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[rt][dt] *= a;
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float p[16];
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          p[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(sc[rt][h][r], scale_log2, -m[rt]));
+      float t[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[e] = p[e] + p[e + 8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] += t[e + 4];
+      lsum[rt] += (t[0] + t[2]) + (t[1] + t[3]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        pf[rt][j] = make_uint4(pack2(p[8 * j + 0], p[8 * j + 1]), pack2(p[8 * j + 2], p[8 * j + 3]),
+                               pack2(p[8 * j + 4], p[8 * j + 5]), pack2(p[8 * j + 6], p[8 * j + 7]));
+    }
+  };
+  // this lane's transposed-read address for V dims 16 dt + 4 (c % 4) .. + 3 of key 16 h + 4 q4 +
+  // c / 4: 16-byte unit 2 dt + (c / 2) % 2, half c % 2
+  auto vt_addr = [&](int buf, int dt, int h) -> const void* {
+    const int key = 16 * h + 4 * q4 + (c >> 2);
+    const int u = 2 * dt + ((c >> 1) & 1);
+    return reinterpret_cast<const char*>(&sm.v[buf][key * 16 + (u ^ (key & 15))]) + 8 * (c & 1);
+  };
+  // O^T += V^T . P^T from the tile in `buf`, per 32-key half j: keys 32 j + 4 q4 .. + 3 and
+  // 32 j + 16 + 4 q4 .. + 3
+  auto pv = [&](int buf, const uint4 (&pf)[2][2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const uint2 lo = lds_read_tr16(vt_addr(buf, dt, 2 * j));
+        const uint2 hi = lds_read_tr16(vt_addr(buf, dt, 2 * j + 1));
+        const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+          o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, vf), __builtin_bit_cast(bf16x8_t, pf[rt][j]),
+              o[rt][dt], 0, 0, 0);
+      }
+    }
+  };
+  // Tile it sits in buffer it % BA_NBUF.  Step it issues the DMA of tile it + BA_NBUF - 2 into the
+  // buffer of tile it - 2 (last read in step it - 1, before its barrier), does its share of the
+  // contraction, then waits for its own DMA of tile it + 1 (the loads of the tiles after it may
+  // stay in flight) and meets the other waves at the barrier, after which tile it + 1 is
+  // visible.  Tiles past ntiles are loaded (valid cache rows) but never consumed.
+  // Waves w and w + 4 share a SIMD.  Waves 0-3 run step it as O += P(it-1) V(it-1), S'(it),
+  // softmax(it) -- MFMA, then VALU -- and waves 4-7 half a step behind as softmax(it-1),
+  // O += P(it-1) V(it-1), S'(it) -- VALU, then MFMA -- so that on every SIMD one wave's MFMAs can
+  // run beside the other's softmax.  Each wave still applies its tiles in order.
+  constexpr int AHEAD = BA_NBUF - 2;
+#pragma unroll
+  for (int i = 0; i < AHEAD; ++i) issue(i, i);
+  wait_vm<4 * (AHEAD - 1)>();
+  lds_barrier();
+  const bool lead = wave < 4;                                // wave-uniform
+  f32x4_t sc[2][4];
+  uint4 pf[2][2];
+  // a tile is visible to every row of the workgroup when it ends below kend and below base --
+  // or, in a causal chunk, below the workgroup's first token (every row sees the block keys
+  // before it)
+  const int64_t open_end = anc ? base : base + tb;
+  auto whole = [&](int it) {
+    const int64_t j0 = start + (int64_t)BA_KT * it;
+    return j0 + BA_KT <= open_end && j0 + BA_KT <= kend;
+  };
+  int buf = 0, bprev = BA_NBUF - 1;                          // tiles it and it - 1
+  for (int it = 0; it < ntiles; ++it) {
+    const int bl = bprev == 0 ? BA_NBUF - 1 : bprev - 1;     // tile it - 2's buffer
+    issue(it + AHEAD, bl);
+    if (lead) {
+      if (it > 0) pv(bprev, pf);
+      scores(buf, sc);
+      if (!whole(it)) mask_tile(start + (int64_t)BA_KT * it, sc);
+      softmax(sc, pf);
+    } else {
+      if (it > 0) {
+        if (!whole(it - 1)) mask_tile(start + (int64_t)BA_KT * (it - 1), sc);
+        softmax(sc, pf);
+        pv(bprev, pf);
+      }
+      scores(buf, sc);
+    }
+    wait_vm<4 * (AHEAD - 1)>();
     lds_barrier();
-    stage(k1, v1);
-    lds_barrier();
-    BA_LD(it + 4, k1, v1);
-    contract(start + 32 * (int64_t)(it + 1));
-    lds_barrier();
-    stage(k2, v2);
-    lds_barrier();
-    BA_LD(it + 5, k2, v2);
-    contract(start + 32 * (int64_t)(it + 2));
+    bprev = buf;
+    buf = buf == BA_NBUF - 1 ? 0 : buf + 1;
   }
-  if (it < ntiles) {
-    lds_barrier();
-    stage(k0, v0);
-    lds_barrier();
-    contract(start + 32 * (int64_t)it);
+  if (ntiles > 0) {                                          // the last tile's O update
+    if (!lead) {
+      if (!whole(ntiles - 1)) mask_tile(start + (int64_t)BA_KT * (ntiles - 1), sc);
+      softmax(sc, pf);
+    }
+    pv(bprev, pf);
   }
-  if (it + 1 < ntiles) {
-    lds_barrier();
-    stage(k1, v1);
-    lds_barrier();
-    contract(start + 32 * (int64_t)(it + 1));
-  }
-#undef BA_LD
-  // per-row totals: the four q lanes of a row hold disjoint key subsets of l
+  wait_vm<0>();                                              // no DMA outlives the workgroup
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     float l = lsum[rt];
@@ -377,9 +458,8 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
     if (tok[rt] >= T) continue;
     const int64_t idx = ((b * T + tok[rt]) * Hq + kvh * GRP + head) * splits + split;
     if (splits == 1) {
-      // one key split: the row is complete here.  attn_merge_kernel over one split computes
-      // acc * (1 / l) (its weight exp(m - m) = 1 and sum l are exact), so this store is
-      // bit-identical to the partials + merge it replaces
+      // one key split: the row is complete here (attn_merge_kernel over one split computes
+      // the same acc * (1 / l))
       const float inv = 1.0f / l;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
@@ -392,7 +472,7 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
       *reinterpret_cast<f32x4_t*>(ws_acc + idx * 128 + 16 * dt + 4 * q4) = o[rt][dt];
-    if (q4 == 0) { ws_ml[idx * 2] = m[rt]; ws_ml[idx * 2 + 1] = l; }
+    if (q4 == 0) { ws_ml[idx * 2] = m[rt] * BA_LN2; ws_ml[idx * 2 + 1] = l; }
   }
 }
 
@@ -499,7 +579,8 @@ void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_c
   use = (cap + chunk - 1) / chunk;                      // no empty trailing split
   block_attn_mfma_kernel<<<dim3((unsigned)use, (unsigned)Hkv, (unsigned)(B * QB)), dim3(512), 0,
                            s>>>(q, k_cache, v_cache, base, anc, T, Hq, Hkv, cap, chunk,
-                                1.0f / sqrtf(128.0f), ws_acc, ws_ml, out);
+                                (1.0f / sqrtf(128.0f)) * 1.44269504088896341f, ws_acc, ws_ml,
+                                out);
   if (use > 1)      // one split writes its rows itself
     attn_merge_kernel<<<dim3((unsigned)(B * T * Hq)), dim3(64), 0, s>>>(ws_acc, ws_ml, (int)use,
                                                                         out);

@@ -526,32 +526,6 @@ constexpr int BIG_NBUF = QD_BIG_NBUF;        // LDS stage buffers (BIG_NBUF x 32
 static_assert(BIG_NBUF >= 2 && BIG_NBUF <= 5, "stage buffers");
 
 // LDS byte address of a __shared__ object
-__device__ __forceinline__ uint32_t lds_u32(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-// lane l's 16 bytes at base + voff go to LDS byte lds + 16 l (wave-uniform lds).  Issued as
-// inline asm so that the compiler, which would otherwise wait for every outstanding LDS DMA
-// before any later LDS read, leaves the waits to the explicit vmcnt counts of the stage loop.
-// The s_nop keeps a wait state between the compiler's M0 write and the load.
-__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds)
-               : "memory");
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-// wait until at most PER * C of this wave's loads are outstanding, C = min(n, CMAX)
-template <int PER, int CMAX>
-__device__ __forceinline__ void wait_stages(int n) {
-  if constexpr (CMAX == 0) {
-    wait_vm<0>();
-  } else {
-    if (n >= CMAX) wait_vm<PER * CMAX>();
-    else wait_stages<PER, CMAX - 1>(n);
-  }
-}
-
 // 8 waves (two per SIMD), two along the activation rows and four along the weight rows: wave
 // (wm, wn) owns activation rows 128 wm .. and weight rows 64 wn .. (8 x 4 MFMA tiles, 128 fp32
 // accumulators per lane).  SwiGLU: a wave's 64 weight rows are 32 gate rows and the 32 up rows
