@@ -691,35 +691,46 @@ __global__ __launch_bounds__(BIG_WAVES * 64, 1) void gemm_big_kernel(
 }
 
 // ------------------------------------------------------------------ all rows per workgroup (65..256)
-// At a few hundred activation rows (a tree-verification forward: B x T = 256) the 128 x 128 tiles
-// give 304 gate/up workgroups for 256 CUs (48 CUs run two) and read every weight byte once per
-// 128 rows.  Here a workgroup owns a block of weight rows for all of the (<= 256) activation rows:
-// the blocks are the skinny GEMM's plan (skinny_rows: one round of workgroups) and the K splits
-// the tiled kernel's (gemm_tile_splits, the same K ranges), so the sums -- and the bits -- are the
-// tiled kernel's.  8 waves, wave w the 32 activation rows 32 w .. (2 x NT MFMA tiles; SwiGLU:
-// NT gate tiles and the NT up tiles of the same outputs); K in stages of 64 that go from global
-// memory straight into LDS (128-byte rows, unit u at u ^ (row & 7); the weight rows shared by
-// the waves), RW_NBUF stage buffers, RW_NBUF - 1 stages in flight, one barrier per stage.
-// Measured on a config-5 verify (256 rows): gate/up 58.6 -> 47.3 us, qkv 22.7 -> 20.3 us, o /
-// down unchanged; stages of 32 in 7-8 buffers (twice the bytes in flight, twice the barriers)
-// were slower (8.16 against 7.19 ms per verify).
-constexpr int RW_MAXM = 256;                // activation rows per workgroup (8 waves x 32)
+// At a few hundred activation rows (a tree-verification forward: B x T = 256) a workgroup owns a
+// block of weight rows for 128 MT of the activation rows (all of them, or one of two halves):
+// 8 waves, wave w the 16 MT activation rows 16 MT w .. (NT x MT MFMA tiles; SwiGLU: NT gate
+// tiles and the NT up tiles of the same outputs); K in stages of 64 that go from global memory
+// straight into LDS (128-byte rows, unit u at u ^ (row & 7); the weight rows shared by the
+// waves), RW_NBUF stage buffers, RW_NBUF - 1 stages in flight, one barrier per stage.  Every
+// workgroup re-reads its activation rows' K range from L2, so the plan (rows_plan below) trades
+// those re-reads against more K splits (fp32 partials for the consumer) or activation halves
+// (each weight block read by two workgroups on one XCD, so the second read hits its L2).
+// Measured on a config-5 verify (256 rows) against the 128 x 128 tiles: gate/up 58.6 -> 47.3 us,
+// qkv 22.7 -> 20.3 us with the tiled kernel's split counts; stages of 32 in 7-8 buffers (twice
+// the bytes in flight, twice the barriers) were slower (8.16 against 7.19 ms per verify).
+constexpr int RW_MAXM = 256;                // activation rows per workgroup at most (8 waves x 32)
 constexpr int RW_NBUF = 3;
 
-template <int EPI, bool SPLIT, int NT>
+template <int EPI, bool SPLIT, int NT, int MT>
 __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
     const bf16_t* __restrict__ X, int64_t x_stride, int M, const bf16_t* __restrict__ W, int N,
-    int K, int rows_per_wg, int S, int ks_per, bf16_t* out, int64_t out_stride, const bf16_t* res,
-    int64_t res_stride, float* part) {
+    int K, int rows_per_wg, int S, int ks_per, int mh, bf16_t* out, int64_t out_stride,
+    const bf16_t* res, int64_t res_stride, float* part) {
   constexpr bool SW = EPI == EPI_SWIGLU;
   constexpr int WT = SW ? 2 * NT : NT;       // weight tiles (gate tiles, then up tiles)
   constexpr int WR = 16 * WT;                // staged weight rows
-  constexpr int ROWS = WR + RW_MAXM;         // staged rows per stage (weights, then activations)
+  constexpr int RM = 128 * MT;               // staged activation rows
+  constexpr int ROWS = WR + RM;              // staged rows per stage (weights, then activations)
   constexpr int NBLK = ROWS / 8;             // 1 KiB load blocks per stage (8 rows x 128 bytes)
   constexpr int PER = (NBLK + 7) / 8;        // loads per wave per stage (the last wraps around)
   __shared__ uint4 sm[RW_NBUF][ROWS * 8];
-  const int g = blockIdx.x;
-  const int rb = g / S, split = g - rb * S;
+  // workgroup -> (weight block, K split, activation half): the halves of one weight block are
+  // workgroups g and g + 8 (dispatch puts workgroup g on XCD g % 8), so they share an L2
+  const int nb = (N + rows_per_wg - 1) / rows_per_wg;
+  int blkid = blockIdx.x, mb = 0;
+  if (mh > 1) {
+    const int slot = blockIdx.x >> 3;
+    mb = slot % mh;
+    blkid = (slot / mh) * 8 + (blockIdx.x & 7);
+    if (blkid >= nb * S) return;             // the grid's padding to whole groups of 8
+  }
+  const int rb = blkid / S, split = blkid - rb * S;
+  const int m0 = mb * RM;
   const int n0 = rb * rows_per_wg;
   const int nrows = min(rows_per_wg, N - n0);
   const int ksteps = K / TK;
@@ -728,7 +739,7 @@ __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: load bases in SGPRs
   const int c = lane & 15, q = lane >> 4;
   // LDS row r < WR: weight row n0 + r (SwiGLU: gate rows, then up rows + N); r >= WR: activation
-  // row r - WR; rows past the block / past M reload a valid row (never stored)
+  // row m0 + r - WR; rows past the block / past M reload a valid row (never stored)
   auto grow_off = [&](int r) -> uint32_t {
     if (r < WR) {
       int wr = SW ? (r % (16 * NT)) : r;
@@ -736,7 +747,7 @@ __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
       const int64_t row = (int64_t)n0 + wr + ((SW && r >= 16 * NT) ? N : 0);
       return (uint32_t)(row * K * 2);
     }
-    const int xm = min(r - WR, M - 1);
+    const int xm = min(m0 + r - WR, M - 1);
     return (uint32_t)((int64_t)xm * x_stride * 2);
   };
   // wave w loads blocks w, w + 8, ... (mod NBLK); lane l of a block: row l / 8, position l % 8,
@@ -758,26 +769,26 @@ __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
     for (int j = 0; j < PER; ++j)
       dma16(blk[j] * 8 < WR ? wb : xb, voff[j], l + (uint32_t)blk[j] * 1024);
   };
-  f32x4_t acc[WT][2];
+  f32x4_t acc[WT][MT];
 #pragma unroll
   for (int t = 0; t < WT; ++t)
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) acc[t][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const bool active = 32 * wave < M;         // uniform per wave
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const bool active = m0 + 16 * MT * wave < M;   // uniform per wave
   auto compute = [&](int buf) {
     const uint4* b0 = sm[buf];
 #pragma unroll
     for (int s_ = 0; s_ < 2; ++s_) {
       const int u_ = (4 * s_ + q) ^ (c & 7);
-      uint4 a_[WT], b_[2];
+      uint4 a_[WT], b_[MT];
 #pragma unroll
       for (int t = 0; t < WT; ++t) a_[t] = b0[(16 * t + c) * 8 + u_];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) b_[mt] = b0[(WR + 32 * wave + 16 * mt + c) * 8 + u_];
+      for (int mt = 0; mt < MT; ++mt) b_[mt] = b0[(WR + 16 * MT * wave + 16 * mt + c) * 8 + u_];
 #pragma unroll
       for (int t = 0; t < WT; ++t)
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
           acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(a_[t]), as_bf8(b_[mt]),
                                                                acc[t][mt], 0, 0, 0);
     }
@@ -801,10 +812,10 @@ __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
   }
 
   // epilogue: lane (c, q) of acc[t][mt] holds weight rows 4 q + r of tile t = output columns
-  // n .. n + 3 of activation row m = 32 wave + 16 mt + c
+  // n .. n + 3 of activation row m = m0 + 16 MT wave + 16 mt + c
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int64_t m = 32 * wave + 16 * mt + c;
+  for (int mt = 0; mt < MT; ++mt) {
+    const int64_t m = m0 + 16 * MT * wave + 16 * mt + c;
     if (m >= M) continue;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -879,38 +890,110 @@ int gemm_tile_splits(int64_t M, int64_t N, int64_t K, int epi) {
   return sp < 1 ? 1 : (int)sp;
 }
 
-// The all-rows kernel's plan for M <= 256 rows: blocks of `rows` output rows (the skinny
-// GEMM's rule for this split count), taken when a block is at most 4 MFMA tiles (SwiGLU: 3
-// gate + 3 up) and the blocks fit one round of workgroups.
-static bool rows_plan(int64_t M, int64_t N, int64_t K, int epi, int splits, int& rows, int& nt) {
+// The all-rows kernel's plan for M <= 256 rows.  One round of workgroups; each workgroup moves
+// (through its CU's L1 -> L2 request stream, which bounds this kernel) its weight rows' and its
+// activation rows' K range, and with K splits writes fp32 partials that the consumer reads
+// back.  The plan minimises that per-workgroup traffic over the K split count S (store /
+// residual epilogues, when the caller takes partials), the activation halves (1 or 2) and the
+// block height (a multiple of 4 rows, at most RW_NT_MAX MFMA tiles, the skinny GEMM's rule for
+// the resulting workgroup count):
+//   2 (K / S) (activation rows + weight rows) + [S > 1] 4 (activation rows x block rows
+//   + S M N / CUs).
+// On a config-5 verify (256 rows, 256 CUs) that picks two activation halves for every
+// projection: qkv 96-row blocks in 2 K splits, o and down 124-row blocks in 6, gate/up 76 + 76
+// rows (SwiGLU, no split); the four launches went from 105.9 to 98.7 us per layer (one half per
+// workgroup for gate/up only: 6.86 against 6.63 ms per verify).
+struct RowsPlan {
+  int rows = 0, nt = 0, mt = 0, mh = 0, splits = 0, ks_per = 0;
+};
+constexpr int RW_NT_MAX = 8, RW_NT_MAX_SW = 5;
+
+static int rows_nt_round(int nt, bool sw) {   // the instantiated block heights (MFMA tiles)
+  if (sw) return nt < 2 ? 2 : nt;                              // 2..5
+  if (nt <= 4) return nt;                                      // 1..4
+  return nt <= 6 ? 6 : 8;
+}
+
+static bool rows_plan(int64_t M, int64_t N, int64_t K, int epi, bool can_split, RowsPlan& best) {
+  best = RowsPlan();
   if (!QD_TILE_ROWS || M > RW_MAXM || epi == EPI_ARGMAX) return false;
-  rows = (int)skinny_rows(N, splits);
-  nt = (rows + 15) / 16;
-  if (rows <= 0 || nt > (epi == EPI_SWIGLU ? 3 : 4)) return false;
-  if ((N + rows - 1) / rows * splits > tile_cus()) return false;
-  return (epi == EPI_SWIGLU ? 2 * N : N) * K * 2 < (1ll << 32);
+  const bool sw = epi == EPI_SWIGLU;
+  if ((sw ? 2 * N : N) * K * 2 >= (1ll << 32)) return false;
+  const int64_t cus = tile_cus(), ksteps = K / TK;
+  // the K split count stays the tiled kernel's (more splits measured slower at 256 rows: qkv in
+  // 5 splits 20.2 -> 19.4 us, down in 12 splits 25.5 -> 24.0 us, but their consumers, which
+  // read every split's partials, 8.8 -> 12.0 and 5.3 -> 7.7 us)
+  const int64_t smax = can_split && !sw ? gemm_tile_splits(M, N, K, epi) : 1;
+  double best_cost = 0;
+  for (int mt = 1; mt <= 2; ++mt) {
+    const int64_t rm = 128 * mt, mh = (M + rm - 1) / rm;
+    if (mh > 2 || (mt == 2 && M <= 128)) continue;
+    for (int64_t S0 = smax; S0 <= smax; ++S0) {
+      const int64_t ks_per = (ksteps + S0 - 1) / S0, S = (ksteps + ks_per - 1) / ks_per;
+      const int64_t per = cus / (S * mh);                      // weight blocks in one round
+      if (per < 1) break;
+      const int64_t rows = ((N + per - 1) / per + 3) / 4 * 4;
+      const int nt = rows_nt_round((int)((rows + 15) / 16), sw);
+      const int ntmax = sw ? RW_NT_MAX_SW : S > 1 ? RW_NT_MAX : 4;   // instantiated heights
+      if (nt > ntmax || 16 * nt < rows) continue;
+      const int64_t wgs = (N + rows - 1) / rows * S * mh;
+      if (wgs > cus) continue;
+      const double act = (double)(M < rm ? M : rm), wrows = (double)rows * (sw ? 2 : 1);
+      double cost = 2.0 * ks_per * TK * (act + wrows);
+      if (S > 1) cost += 4.0 * act * rows + 4.0 * S * M * N / cus;
+      if (best.splits == 0 || cost < best_cost) {
+        best_cost = cost;
+        best.rows = (int)rows; best.nt = nt; best.mt = mt; best.mh = (int)mh;
+        best.splits = (int)S; best.ks_per = (int)ks_per;
+      }
+    }
+  }
+  return best.splits > 0;
 }
 
 template <int EPI, bool SPLIT>
-static void launch_rows(int nt, const bf16_t* x, int64_t xs, int M, const bf16_t* w, int N, int K,
-                        int rows, int splits, int ks_per, bf16_t* out, int64_t os,
-                        const bf16_t* res, int64_t rs, float* part, hipStream_t s) {
-  const dim3 g((unsigned)((N + rows - 1) / rows * splits)), b(512);
-#define QD_RW(NT) \
-  gemm_rows_kernel<EPI, SPLIT, NT><<<g, b, 0, s>>>(x, xs, M, w, N, K, rows, splits, ks_per, out, os, res, rs, part)
-  switch (nt) {
-    case 1: QD_RW(1); break;
-    case 2: QD_RW(2); break;
-    case 3: QD_RW(3); break;
-    default:
-      if constexpr (EPI != EPI_SWIGLU) QD_RW(4);
-      break;
+static void launch_rows(const RowsPlan& P, const bf16_t* x, int64_t xs, int M, const bf16_t* w,
+                        int N, int K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs,
+                        float* part, hipStream_t s) {
+  const int nblk = (N + P.rows - 1) / P.rows * P.splits;
+  const int ng = P.mh > 1 ? (nblk + 7) / 8 * 8 * P.mh : nblk;
+  const dim3 g((unsigned)ng), b(512);
+#define QD_RW(NT, MT)                                                                           \
+  gemm_rows_kernel<EPI, SPLIT, NT, MT><<<g, b, 0, s>>>(x, xs, M, w, N, K, P.rows, P.splits,       \
+                                                       P.ks_per, P.mh, out, os, res, rs, part)
+#define QD_RW_MT(NT) \
+  do { if (P.mt == 1) QD_RW(NT, 1); else QD_RW(NT, 2); } while (0)
+  if constexpr (EPI == EPI_SWIGLU) {
+    switch (P.nt) {
+      case 2: QD_RW_MT(2); break;
+      case 3: QD_RW_MT(3); break;
+      case 4: QD_RW_MT(4); break;
+      default: QD_RW_MT(5); break;
+    }
+  } else if constexpr (SPLIT) {
+    switch (P.nt) {
+      case 1: QD_RW_MT(1); break;
+      case 2: QD_RW_MT(2); break;
+      case 3: QD_RW_MT(3); break;
+      case 4: QD_RW_MT(4); break;
+      case 6: QD_RW_MT(6); break;
+      default: QD_RW_MT(8); break;
+    }
+  } else {
+    switch (P.nt) {
+      case 1: QD_RW_MT(1); break;
+      case 2: QD_RW_MT(2); break;
+      case 3: QD_RW_MT(3); break;
+      default: QD_RW_MT(4); break;
+    }
   }
+#undef QD_RW_MT
 #undef QD_RW
 }
 
 int64_t gemm_tile_ws_floats(int64_t M, int64_t N, int64_t K, int epi) {
-  const int sp = gemm_tile_splits(M, N, K, epi);
+  RowsPlan P;
+  const int sp = rows_plan(M, N, K, epi, true, P) ? P.splits : gemm_tile_splits(M, N, K, epi);
   return sp > 1 ? (int64_t)sp * M * N : 0;
 }
 
@@ -921,17 +1004,20 @@ int gemm_tile_partials(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, 
   if (M < GEMM_TILE_MIN_M || !part ||
       !gemm_tile_ok(M, N, K, EPI_NONE, x, xs, w, part, N, nullptr, 0))
     return 0;
+  RowsPlan P;
+  if (rows_plan(M, N, K, EPI_NONE, true, P)) {
+    if (P.splits <= 1 || part_floats < (int64_t)P.splits * M * N) return 0;
+    launch_rows<EPI_NONE, true>(P, x, xs, (int)M, w, (int)N, (int)K, nullptr, 0, nullptr, 0,
+                                part, s);
+    return P.splits;
+  }
   int splits = gemm_tile_splits(M, N, K, EPI_NONE);
   if (splits <= 1 || part_floats < (int64_t)splits * M * N) return 0;
   const int ksteps = (int)(K / TK);
   const int ks_per = (ksteps + splits - 1) / splits;
   splits = (ksteps + ks_per - 1) / ks_per;              // no empty split
   const int64_t mblocks = (M + TM - 1) / TM, nblocks = tile_nblocks(N, EPI_NONE);
-  int rw_rows = 0, rw_nt = 0;
-  if (rows_plan(M, N, K, EPI_NONE, splits, rw_rows, rw_nt))
-    launch_rows<EPI_NONE, true>(rw_nt, x, xs, (int)M, w, (int)N, (int)K, rw_rows, splits, ks_per,
-                                nullptr, 0, nullptr, 0, part, s);
-  else if (QD_TILE8)
+  if (QD_TILE8)
     gemm_tile8_kernel<EPI_NONE, true><<<dim3((unsigned)(mblocks * nblocks * splits)), dim3(512), 0, s>>>(
         x, xs, (int)M, w, (int)N, (int)K, (int)mblocks, (int)nblocks, ks_per, nullptr, 0, nullptr,
         0, part);
@@ -960,6 +1046,32 @@ int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w
 #undef QD_BIG
     return 0;
   }
+  if (epi != EPI_ARGMAX) {
+    RowsPlan P;
+    if (rows_plan(M, N, K, epi, true, P) && P.splits > 1 &&
+        (!part || part_floats < (int64_t)P.splits * M * N))
+      rows_plan(M, N, K, epi, false, P);                      // no room for partials: S = 1
+    if (P.splits > 1) {
+      launch_rows<EPI_NONE, true>(P, x, xs, (int)M, w, (int)N, (int)K, nullptr, 0, nullptr, 0,
+                                  part, s);
+      const int64_t thr = M * (N / 4);
+      const dim3 rg((unsigned)((thr + 255) / 256)), rb(256);
+      if (epi == EPI_RES)
+        gemm_split_reduce_kernel<EPI_RES><<<rg, rb, 0, s>>>(part, P.splits, M, N, out, os, res, rs);
+      else
+        gemm_split_reduce_kernel<EPI_NONE><<<rg, rb, 0, s>>>(part, P.splits, M, N, out, os, res, rs);
+      return 0;
+    }
+    if (P.splits == 1) {
+      if (epi == EPI_RES)
+        launch_rows<EPI_RES, false>(P, x, xs, (int)M, w, (int)N, (int)K, out, os, res, rs, part, s);
+      else if (epi == EPI_SWIGLU)
+        launch_rows<EPI_SWIGLU, false>(P, x, xs, (int)M, w, (int)N, (int)K, out, os, res, rs, part, s);
+      else
+        launch_rows<EPI_NONE, false>(P, x, xs, (int)M, w, (int)N, (int)K, out, os, res, rs, part, s);
+      return 0;
+    }
+  }
   const int64_t mblocks = (M + TM - 1) / TM, nblocks = tile_nblocks(N, epi);
   int splits = gemm_tile_splits(M, N, K, epi);
   if (splits > 1 && (!part || part_floats < (int64_t)splits * M * N)) splits = 1;
@@ -968,14 +1080,9 @@ int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w
   splits = (ksteps + ks_per - 1) / ks_per;              // no empty split
   const dim3 grid((unsigned)(mblocks * nblocks * splits)), block(256);
   const int Mi = (int)M, Ni = (int)N, Ki = (int)K, mbi = (int)mblocks, nbi = (int)nblocks;
-  int rw_rows = 0, rw_nt = 0;
-  const bool rw = rows_plan(M, N, K, epi, splits, rw_rows, rw_nt);
 #define QD_TILE(E, SP)                                                                           \
   do {                                                                                           \
-    if (rw && E != EPI_ARGMAX)                                                                   \
-      launch_rows<E == EPI_ARGMAX ? EPI_NONE : E, SP>(rw_nt, x, xs, Mi, w, Ni, Ki, rw_rows,      \
-                                                      splits, ks_per, out, os, res, rs, part, s); \
-    else if (QD_TILE8 && E != EPI_ARGMAX)                                                        \
+    if (QD_TILE8 && E != EPI_ARGMAX)                                                             \
       gemm_tile8_kernel<E == EPI_ARGMAX ? EPI_NONE : E, SP><<<grid, dim3(512), 0, s>>>(          \
           x, xs, Mi, w, Ni, Ki, mbi, nbi, ks_per, out, os, res, rs, part);                       \
     else                                                                                         \
