@@ -156,13 +156,13 @@ def tree_run(eng, B=4, S=8192, T=64, K=20, warmup=3, N_e2e=64, seed=5):
         run.anc.copy_(torch.tensor([t.anc_i64() for t in trees], dtype=torch.int64))
         run.base.fill_(S)
         for _ in range(warmup):
-            run.enqueue(T)
+            run.launch(T)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(st):
         e0.record(st)
         for _ in range(K):
-            run.enqueue(T)
+            run.launch(T)
         e1.record(st)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / K

@@ -70,7 +70,7 @@ class _Shape:
             pr.tokens.view(-1)[:B * T].view(B, T).copy_(self.ids[:, c0:c0 + T])
             pr.base.fill_(c0)
             # only the chunk holding the last prompt token needs the LM head
-            pr.enqueue(T, lm_mode=_lib.LM_LAST if c0 + T == S else _lib.LM_NONE)
+            pr.launch(T, lm_mode=_lib.LM_LAST if c0 + T == S else _lib.LM_NONE)
         self.kv.tok.copy_(pr.out_tok)
 
 

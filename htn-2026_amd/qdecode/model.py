@@ -285,6 +285,8 @@ class BlockRunner:
     """T_max tokens per sequence through every layer (qd_block_step): causal prompt chunks
     (prefill) or tree verification with ancestor masks."""
 
+    use_graphs = True        # launch() replays recorded hipGraphs (False: kernel by kernel)
+
     def __init__(self, kv, stream, t_max, causal, lm_mode):
         m = kv.model
         self.kv, self.model, self.stream = kv, m, stream
@@ -305,7 +307,11 @@ class BlockRunner:
         self.out_tok = z(M if lm_mode == _lib.LM_ALL else B)
         nbytes = _lib.LIB.qd_block_workspace_bytes(C.byref(m.qd), B, t_max, kv.cap)
         self.ws = torch.zeros((nbytes,), dtype=torch.uint8, device=dev)
-        self.graph = None
+        # hipGraphs of the forward, one per (T, compact, lm_mode): the forward reads every input
+        # (tokens, base, depth, anc, compaction lists) from these device buffers, so a replay
+        # after the buffers are rewritten runs the new inputs (engine.py:685-713 captures its
+        # prefill / verify / tree forwards the same way)
+        self.graphs = {}
 
     def state(self, T, compact=False, lm_mode=None):
         kv = self.kv
@@ -321,11 +327,44 @@ class BlockRunner:
             self.attn.data_ptr(), self.act.data_ptr(), self.ws.data_ptr(), self.ws.numel())
 
     def enqueue(self, T=None, compact=False, lm_mode=None):
+        """One forward, launched kernel by kernel on the runner's stream."""
         T = self.t_max if T is None else T
         if not 0 < T <= self.t_max:
             raise ValueError(f"T={T} outside (0, {self.t_max}]")
         st = self.state(T, compact, lm_mode)
         _lib.call("qd_block_step", C.byref(self.model.qd), C.byref(st), self.stream.cuda_stream)
+
+    def launch(self, T=None, compact=False, lm_mode=None):
+        """One forward as a graph replay (recorded on the first call with these arguments), or
+        kernel by kernel when use_graphs is off.  Same kernels, same bits either way."""
+        T = self.t_max if T is None else T
+        if not self.use_graphs:
+            return self.enqueue(T, compact, lm_mode)
+        key = (T, bool(compact), self.lm_mode if lm_mode is None else lm_mode)
+        g = self.graphs.get(key)
+        if g is None:
+            s = self.stream.cuda_stream
+            _lib.call("qd_graph_begin", s)
+            try:
+                self.enqueue(T, compact, lm_mode)
+            finally:
+                ex = C.c_void_p()
+                rc = _lib.LIB.qd_graph_end(s, C.byref(ex))
+            if rc != 0:
+                raise _lib.QDError("qd_graph_end", rc)
+            g = self.graphs[key] = ex
+        _lib.call("qd_graph_launch", g, self.stream.cuda_stream)
+
+    def close(self):
+        for g in self.graphs.values():
+            _lib.LIB.qd_graph_destroy(g)
+        self.graphs = {}
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 # Rows per causal prefill forward.  6144 = 24 blocks of the prefill GEMM's 256-row tiles, so the

@@ -171,7 +171,7 @@ def stream_tree(engine, sh, ids, N, drafter):
             for d, h in ((tr.tokens, h_tok), (tr.depth, h_depth), (tr.anc, h_anc), (tr.base, h_base),
                          (tr.c_base, h_cb), (tr.c_src, h_cs), (tr.c_cnt, h_cc)):
                 d.copy_(h, non_blocking=True)
-            tr.enqueue(T, compact=True)
+            tr.launch(T, compact=True)
             h_out.copy_(tr.out_tok, non_blocking=True)
             ev.record(stream)
         ev.synchronize()

@@ -222,6 +222,48 @@ def test_generate_tree_modes(eng2, ref2):
         eng2.tree_mode, eng2.tree_on = mode, {}
 
 
+def test_block_forward_graphs_match_eager(eng2):
+    """The prefill and tree-verify forwards replayed from hipGraphs (one per (T, compaction, LM
+    mode), recorded on first use) emit exactly the ids of the same forwards launched kernel by
+    kernel.  Every tree pass rewrites the runner's input buffers (tokens, base, depths, masks,
+    compaction lists) with host copies and synchronises on its output before the next replay,
+    and each later pass depends on every earlier pass's accepted tokens and compacted K/V, so
+    comparing the streams checks every replay against eager execution; the second graph run on
+    a shape replays the graphs the first one recorded."""
+    say("graphs vs eager: generate_tree B=4 S=40 N=12 (random drafts), generate B=2 S=200 in "
+        "two prefill chunks")
+    from qdecode import model as M
+    from qdecode import tree as tr
+    prompt = synth.prompt_ids(51, 4, 40).tolist()
+    prompt2 = synth.prompt_ids(52, 2, 200).tolist()
+    mode = eng2.tree_mode
+    runs = {}
+    try:
+        eng2.tree_mode = "0"
+        for use in (False, True):
+            M.BlockRunner.use_graphs = use
+            eng2.shape = None
+            t = [list(eng2.generate_tree(prompt, 12, tr.random_tree_drafter(3), T=64))
+                 for _ in range(2)]
+            ntree = len(eng2.shape.tree.graphs) + len(eng2.shape.prefill.graphs)
+            eng2.prefill_budget_rows = 256                  # two causal chunks of 128 tokens
+            eng2.shape = None
+            p = [list(eng2.generate(prompt2, 8)) for _ in range(2)]
+            npre = len(eng2.shape.prefill.graphs)
+            eng2.prefill_budget_rows = None
+            runs[use] = (t, p, ntree, npre)
+    finally:
+        M.BlockRunner.use_graphs = True
+        eng2.tree_mode = mode
+        eng2.prefill_budget_rows = None
+        eng2.shape = None
+    te, pe, nte, npe = runs[False]
+    tg, pg, ntg, npg = runs[True]
+    assert nte == npe == 0 and ntg == 2 and npg == 2     # tree: prefill + verify; 2 chunks
+    assert te[0] == te[1] == tg[0] == tg[1]
+    assert pe[0] == pe[1] == pg[0] == pg[1]
+
+
 def _device_bits(t):
     return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
 
