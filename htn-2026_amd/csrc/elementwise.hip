@@ -279,7 +279,7 @@ constexpr int QKR_ROWS = 2 * QKR_RPG;   // token rows per workgroup
 // PART: the packed qkv rows are the split-K partials of the qkv projection, part[S][B*T][width]
 // fp32 (the tiled GEMM's split layout): each value is their sum in split order rounded to
 // bf16, the same bits gemm_split_reduce_kernel would have stored.
-template <bool PART>
+template <bool PART, int SC = 0>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const bf16_t* __restrict__ qkv, int64_t qkv_stride, const bf16_t* __restrict__ qn,
     const bf16_t* __restrict__ kn, const bf16_t* __restrict__ cos_t,
@@ -311,15 +311,35 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
         v[2 * h] = p0[0];
         v[2 * h + 1] = p0[1];
       }
-      for (int sp = 1; sp < S; ++sp) {
+      if constexpr (SC > 1) {
+        // the split count at compile time: every split's loads issue before the first add
+        float4 w[SC - 1][4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const float4* ps = reinterpret_cast<const float4*>(part + (int64_t)sp * rows_total * width + col + 64 * h);
-          const float4 a2 = ps[0], b2 = ps[1];
-          float4& a = v[2 * h];
-          float4& c = v[2 * h + 1];
-          a.x += a2.x; a.y += a2.y; a.z += a2.z; a.w += a2.w;
-          c.x += b2.x; c.y += b2.y; c.z += b2.z; c.w += b2.w;
+        for (int sp = 1; sp < SC; ++sp)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float4* ps = reinterpret_cast<const float4*>(part + (int64_t)sp * rows_total * width + col + 64 * h);
+            w[sp - 1][2 * h] = ps[0];
+            w[sp - 1][2 * h + 1] = ps[1];
+          }
+#pragma unroll
+        for (int sp = 1; sp < SC; ++sp)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e].x += w[sp - 1][e].x; v[e].y += w[sp - 1][e].y;
+            v[e].z += w[sp - 1][e].z; v[e].w += w[sp - 1][e].w;
+          }
+      } else {
+        for (int sp = 1; sp < S; ++sp) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float4* ps = reinterpret_cast<const float4*>(part + (int64_t)sp * rows_total * width + col + 64 * h);
+            const float4 a2 = ps[0], b2 = ps[1];
+            float4& a = v[2 * h];
+            float4& c = v[2 * h + 1];
+            a.x += a2.x; a.y += a2.y; a.z += a2.z; a.w += a2.w;
+            c.x += b2.x; c.y += b2.y; c.z += b2.z; c.w += b2.w;
+          }
         }
       }
       xl[i] = make_uint4(pack2(v[0].x, v[0].y), pack2(v[0].z, v[0].w), pack2(v[1].x, v[1].y), pack2(v[1].z, v[1].w));
@@ -473,9 +493,15 @@ void launch_qk_norm_rope_part(const float* part, int S, const bf16_t* qn, const 
   if (B * T <= 0) return;
   const dim3 grid((unsigned)((T + QKR_ROWS - 1) / QKR_ROWS), (unsigned)B,
                   (unsigned)((Hq + 2 * Hkv + 15) / 16));
-  qk_norm_rope_kernel<true><<<grid, dim3(256), 0, s>>>(nullptr, 0, qn, kn, cos_t, sin_t, table_len,
-                                                       pos, depth, mode, q_out, k_cache, v_cache, T,
-                                                       Hq, Hkv, cap, eps, part, S, B * T);
+  if (S == 2)
+    qk_norm_rope_kernel<true, 2><<<grid, dim3(256), 0, s>>>(nullptr, 0, qn, kn, cos_t, sin_t,
+                                                            table_len, pos, depth, mode, q_out,
+                                                            k_cache, v_cache, T, Hq, Hkv, cap, eps,
+                                                            part, S, B * T);
+  else
+    qk_norm_rope_kernel<true><<<grid, dim3(256), 0, s>>>(nullptr, 0, qn, kn, cos_t, sin_t, table_len,
+                                                         pos, depth, mode, q_out, k_cache, v_cache,
+                                                         T, Hq, Hkv, cap, eps, part, S, B * T);
 }
 
 // ------------------------------------------------------------------ SwiGLU
