@@ -53,6 +53,9 @@ constexpr int BIG_GROUP_M = QD_BIG_GROUP_M;
 #ifndef QD_TILE_ROWS
 #define QD_TILE_ROWS 1     // all-rows kernel at 65..256 rows
 #endif
+#ifndef QD_BIG_ARGMAX_MIN_M
+#define QD_BIG_ARGMAX_MIN_M 129   // LM head rows from which the 256 x 256 argmax tile is used
+#endif
 #ifndef QD_BIG_EPIS
 #define QD_BIG_EPIS 7     // epilogues (bit EPI_NONE, EPI_RES, EPI_SWIGLU) that take the big tile
 #endif
@@ -537,7 +540,7 @@ template <int EPI>
 __global__ __launch_bounds__(BIG_WAVES * 64, 1) void gemm_big_kernel(
     const bf16_t* __restrict__ X, int64_t x_stride, int M, const bf16_t* __restrict__ W, int N,
     int K, int mblocks, int nblocks, bf16_t* out, int64_t out_stride, const bf16_t* res,
-    int64_t res_stride) {
+    int64_t res_stride, float* pval, int32_t* pidx, float* logits) {
   constexpr int WAVES = BIG_WAVES;
   constexpr int WN = WAVES / 2;              // waves along the weight rows
   constexpr int NT = BT / WN / 16;           // MFMA tiles per wave along the weight rows
@@ -569,6 +572,9 @@ __global__ __launch_bounds__(BIG_WAVES * 64, 1) void gemm_big_kernel(
   auto wrow = [&](int r) -> int64_t {
     if constexpr (EPI == EPI_SWIGLU) {
       return (int64_t)nb * 128 + HALF * (r / (2 * HALF)) + (r % HALF) + (((r / HALF) & 1) ? N : 0);
+    } else if constexpr (EPI == EPI_ARGMAX) {
+      const int64_t n = (int64_t)nb * BT + r;          // the last block may pass the vocabulary:
+      return n < N ? n : N - 1;                        // reload a valid row, never ranked
     } else {
       return (int64_t)nb * BT + r;
     }
@@ -655,6 +661,59 @@ __global__ __launch_bounds__(BIG_WAVES * 64, 1) void gemm_big_kernel(
 
   // epilogue: lane (c, q) of acc[nt][mt] holds weight rows 4 q + r of tile nt = output columns
   // n .. n + 3 of activation row m = m0 + 128 wm + 16 mt + c
+  if constexpr (EPI == EPI_ARGMAX) {
+    // LM head: per activation row the maximum bf16 logit of the block's 256 vocabulary rows and
+    // its lowest index (the lane's columns ascend with nt and r; lanes and waves hold interleaved
+    // column ranges, so ties compare indices) -> pval / pidx[m][nb] for argmax_reduce_kernel
+    __shared__ float amax_v[2][WN][128];
+    __shared__ int32_t amax_i[2][WN][128];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      const int64_t m = m0 + 128 * wm + 16 * mt + c;
+      float bv = -INFINITY;
+      int32_t bi = 0x7FFFFFFF;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int64_t n = (int64_t)nb * BT + NT * 16 * wn + 16 * nt + 4 * q;
+        if (m < M && logits && n < N)
+          *reinterpret_cast<f32x4_t*>(logits + m * (int64_t)N + n) = acc[nt][mt];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = rbf(acc[nt][mt][r]);
+          if (n + r < N && v > bv) { bv = v; bi = (int32_t)(n + r); }
+        }
+      }
+#pragma unroll
+      for (int sh = 0; sh < 2; ++sh) {
+        const float ov = sh ? lane_xor32(bv) : lane_xor16(bv);
+        const int32_t oi = sh ? __builtin_bit_cast(int32_t, lane_xor32(__builtin_bit_cast(float, bi)))
+                              : __builtin_bit_cast(int32_t, lane_xor16(__builtin_bit_cast(float, bi)));
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      }
+      if (q == 0) {
+        amax_v[wm][wn][16 * mt + c] = bv;
+        amax_i[wm][wn][16 * mt + c] = bi;
+      }
+    }
+    lds_barrier();
+    if (tid < 256) {
+      const int wm2 = tid >> 7, r = tid & 127;
+      const int64_t m = m0 + 128 * wm2 + r;
+      if (m < M) {
+        float bv = amax_v[wm2][0][r];
+        int32_t bi = amax_i[wm2][0][r];
+#pragma unroll
+        for (int w = 1; w < WN; ++w) {
+          const float ov = amax_v[wm2][w][r];
+          const int32_t oi = amax_i[wm2][w][r];
+          if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        pval[m * (int64_t)nblocks + nb] = bv;
+        pidx[m * (int64_t)nblocks + nb] = bi;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt) {
     const int64_t m = m0 + 128 * wm + 16 * mt + c;
@@ -1039,12 +1098,23 @@ int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w
     const int64_t mbl = (M + BT - 1) / BT, nbl = epi == EPI_SWIGLU ? N / 128 : N / BT;
     const dim3 g((unsigned)(mbl * nbl)), b(BIG_WAVES * 64);
 #define QD_BIG(E) \
-  gemm_big_kernel<E><<<g, b, 0, s>>>(x, xs, (int)M, w, (int)N, (int)K, (int)mbl, (int)nbl, out, os, res, rs)
+  gemm_big_kernel<E><<<g, b, 0, s>>>(x, xs, (int)M, w, (int)N, (int)K, (int)mbl, (int)nbl, out, os, res, rs, \
+                                     nullptr, nullptr, nullptr)
     if (epi == EPI_RES) QD_BIG(EPI_RES);
     else if (epi == EPI_SWIGLU) QD_BIG(EPI_SWIGLU);
     else QD_BIG(EPI_NONE);
 #undef QD_BIG
     return 0;
+  }
+  if (epi == EPI_ARGMAX && M >= QD_BIG_ARGMAX_MIN_M && N % 4 == 0 && N >= BT &&
+      N * K * 2 < (1ll << 32) && M * xs * 2 < (1ll << 32)) {
+    // LM head over many rows (a tree verification's 256): 256 x 256 tiles read every weight
+    // byte once per 256 activation rows, half the L2 traffic of the 128 x 128 tiles
+    const int64_t mbl = (M + BT - 1) / BT, nbl = (N + BT - 1) / BT;
+    gemm_big_kernel<EPI_ARGMAX><<<dim3((unsigned)(mbl * nbl)), dim3(BIG_WAVES * 64), 0, s>>>(
+        x, xs, (int)M, w, (int)N, (int)K, (int)mbl, (int)nbl, nullptr, 0, nullptr, 0, pval, pidx,
+        logits);
+    return nbl;
   }
   if (epi != EPI_ARGMAX) {
     RowsPlan P;

@@ -204,8 +204,9 @@ def test_linear_epilogues(ops, name, B):
 
 # ------------------------------------------------------------------ LM head + argmax
 # 1-2 rows: the vector kernel; 3-64: the weight-streaming MFMA kernel (16 / 32 / 64-row
-# activation tiles); 72: the tiled kernel
-@pytest.mark.parametrize("B", [1, 2, 8, 24, 40, 72])
+# activation tiles); 72: the 128 x 128 tiled kernel; 160, 256: the 256 x 256 tile with the argmax
+# epilogue (one partly filled / one full row block, and the vocabulary's last block half full)
+@pytest.mark.parametrize("B", [1, 2, 8, 24, 40, 72, 160, 256])
 def test_lm_head_argmax(ops, B):
     say(f"lm_head_argmax B={B}")
     g = torch.Generator().manual_seed(400 + B)
@@ -234,7 +235,7 @@ def test_lm_head_argmax(ops, B):
     assert int(pos.item()) == 1                                  # position advanced once
 
 
-@pytest.mark.parametrize("B", [1, 8, 40, 72])
+@pytest.mark.parametrize("B", [1, 8, 40, 72, 256])
 def test_lm_head_ties_pick_lowest_index(ops, B):
     say(f"lm_head ties B={B}")
     V, K = 151936, 2560
