@@ -212,10 +212,16 @@ __device__ __forceinline__ void put_pairs(Smem& sm, uint32_t* dst, int64_t w0, i
 }
 
 // ------------------------------------------------------------------ phases
+// The phases take their thread index from hw_tid() (threadIdx.x through an empty asm), so the
+// compiler recomputes the lane offsets derived from it in each phase instead of keeping them
+// live across the layer loop: no VGPR spills (252 VGPRs, no scratch; with threadIdx.x here 16
+// VGPRs went to scratch and the step was 0.25 % slower).  The GEMV helpers above keep
+// threadIdx.x: their offsets are hoisted out of the row loops, and an opaque index there costs
+// 3 % of the step.
 // qkv = RMSNorm(x; ln1) . Wqkv^T   (rows wave, wave + 8, wave + 16 of the workgroup's 24)
 __device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t* ll,
                           int64_t tok) {
-  const int wave = threadIdx.x >> 6;
+  const int wave = hw_tid() >> 6;
   const Layout ly = ll_layout(p.L, p.splits);
   uint32_t* LL = ll + (int64_t)l * ly.per_layer;
   int64_t a, b;
@@ -232,7 +238,7 @@ __device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, u
   if (l == 0) {                    // the embedding row (an id outside the vocab reads zeros)
     const bool ok = tok >= 0 && tok < p.vocab;
     const uint4* src = reinterpret_cast<const uint4*>(p.embed + (ok ? tok : 0) * H);
-    for (int c = threadIdx.x; c < H / 8; c += MG_NT) sm.xs[c] = ok ? src[c] : make_uint4(0, 0, 0, 0);
+    for (int c = hw_tid(); c < H / 8; c += MG_NT) sm.xs[c] = ok ? src[c] : make_uint4(0, 0, 0, 0);
   } else {
     const uint32_t* prev = ll + (int64_t)(l - 1) * ly.per_layer + ly.out;
     ll_fetch_lds<2>(prev, H / 2, p.ctl + 1, xs32);
@@ -241,7 +247,7 @@ __device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, u
   {                                // residual values of this workgroup's o rows
     int64_t oa, ob;
     o_rows(p, wg, P, oa, ob);
-    const int t = threadIdx.x;
+    const int t = hw_tid();
     if (t < 2 * (ob - oa)) sm.rown[t] = bf2f(reinterpret_cast<const bf16_t*>(sm.xs)[2 * oa + t]);
   }
   mg_norm<5, 512>(sm.xs, nw, p.eps, sm.red);
@@ -250,7 +256,7 @@ __device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, u
     const int k = wave + rr * MG_NW;
     if (k < nr) {
       const float acc = mg_dot<5>(w[rr], sm.xs);
-      if ((threadIdx.x & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(acc);
+      if ((hw_tid() & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(acc);
     }
   }
   lds_barrier();
@@ -260,7 +266,7 @@ __device__ void phase_qkv(const MegaParams& p, Smem& sm, int l, int wg, int P, u
 // one decode-attention unit (KV head, split) of layer l
 __device__ void phase_attn_unit(const MegaParams& p, Smem& sm, int l, int unit, uint32_t* ll,
                                 int64_t pos) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = hw_tid() >> 6, lane = hw_tid() & 63;
   const Layout ly = ll_layout(p.L, p.splits);
   uint32_t* LL = ll + (int64_t)l * ly.per_layer;
   const int kvh = unit / p.splits, split = unit % p.splits;
@@ -297,7 +303,7 @@ __device__ void phase_attn_unit(const MegaParams& p, Smem& sm, int l, int unit, 
   auto partial_out = [&](int h, int d, float A0, float A1, float M, float Lsum) {
     const int64_t idx = (int64_t)(kvh * GRP + h) * p.splits + split;
     hw_put2(LL + ly.part + idx * HD + d, __float_as_uint(A0), __float_as_uint(A1));
-    if ((threadIdx.x & 63) == 0)
+    if ((hw_tid() & 63) == 0)
       hw_put2(LL + ly.ml + idx * 2, __float_as_uint(M), __float_as_uint(Lsum));
   };
   decode_attn_unit<ATTN_NW>(sm.attn, fetch, final_out, partial_out,
@@ -308,7 +314,7 @@ __device__ void phase_attn_unit(const MegaParams& p, Smem& sm, int l, int unit, 
 
 // LSE merge of q head hq's split partials (one wave) -> ATT words of the head
 __device__ void phase_merge(const MegaParams& p, int l, int hq, uint32_t* ll) {
-  const int lane = threadIdx.x & 63;
+  const int lane = hw_tid() & 63;
   const Layout ly = ll_layout(p.L, p.splits);
   uint32_t* LL = ll + (int64_t)l * ly.per_layer;
   uint32_t* err = p.ctl + 1;
@@ -344,7 +350,7 @@ __device__ void phase_merge(const MegaParams& p, int l, int hq, uint32_t* ll) {
 // hand-off; later act rows refill the 3-slot ring as rows are consumed.  A workgroup without o
 // rows skips the attention output and goes straight to the MID wait.
 __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t* ll) {
-  const int wave = threadIdx.x >> 6;
+  const int wave = hw_tid() >> 6;
   const Layout ly = ll_layout(p.L, p.splits);
   uint32_t* LL = ll + (int64_t)l * ly.per_layer;
   int64_t a, b;
@@ -379,7 +385,7 @@ __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, 
       const int k = wave + rr * MG_NW;
       if (k < nr) {
         const float acc = mg_dot<8>(w[rr], sm.xs);
-        if ((threadIdx.x & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(sm.rown[k] + rbf(acc));
+        if ((hw_tid() & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(sm.rown[k] + rbf(acc));
       }
     }
     lds_barrier();
@@ -393,7 +399,7 @@ __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, 
   {                                // residual values of this workgroup's down rows
     int64_t da, db;
     part_range(H / 2, wg, P, da, db);
-    const int t = threadIdx.x;
+    const int t = hw_tid();
     if (t < 2 * (db - da))
       sm.rown[t] = bf2f(reinterpret_cast<const bf16_t*>(sm.xs)[2 * da + t]);
   }
@@ -405,7 +411,7 @@ __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, 
       const float ag = mg_dot<5>(g[rr % 3], sm.xs);
       const float au = mg_dot<5>(u[rr % 3], sm.xs);
       if (rr + 3 < RW) load_gu(rr % 3, rr + 3);
-      if ((threadIdx.x & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(rbf(silu_f(rbf(ag))) * rbf(au));
+      if ((hw_tid() & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(rbf(silu_f(rbf(ag))) * rbf(au));
     }
   }
   lds_barrier();
@@ -416,7 +422,7 @@ __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, 
 // workgroup zeroes its share of layer l's words in the other copy (nxt)
 __device__ void phase_down(const MegaParams& p, Smem& sm, int l, int wg, int P, uint32_t* ll,
                            uint32_t* nxt) {
-  const int wave = threadIdx.x >> 6;
+  const int wave = hw_tid() >> 6;
   const Layout ly = ll_layout(p.L, p.splits);
   uint32_t* LL = ll + (int64_t)l * ly.per_layer;
   int64_t a, b;
@@ -436,12 +442,12 @@ __device__ void phase_down(const MegaParams& p, Smem& sm, int l, int wg, int P, 
     const int k = wave + rr * MG_NW;
     if (k < nr) {
       const float acc = mg_dot<19>(w[rr], sm.xs);
-      if ((threadIdx.x & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(sm.rown[k] + rbf(acc));
+      if ((hw_tid() & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(sm.rown[k] + rbf(acc));
     }
   }
   lds_barrier();
   put_pairs(sm, LL + ly.out, a, nr);
-  if (l == p.L - 1 && threadIdx.x < nr) p.x_out[r0 + threadIdx.x] = sm.obuf[threadIdx.x];
+  if (l == p.L - 1 && hw_tid() < nr) p.x_out[r0 + hw_tid()] = sm.obuf[hw_tid()];
 }
 
 // final RMSNorm + LM head over the workgroup's vocab rows: best (bf16 logit, lowest index)
