@@ -213,7 +213,9 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
   const int splits = gridDim.x;
   const int64_t QB = (T + BA_TQ - 1) / BA_TQ;
   const int64_t b = blockIdx.z / QB;
-  const int64_t tb = (blockIdx.z % QB) * BA_TQ;             // the workgroup's first token
+  // query blocks in descending order: under a causal mask the later blocks hold the most keys,
+  // and starting them first leaves the short ones for the end of the launch
+  const int64_t tb = (QB - 1 - blockIdx.z % QB) * BA_TQ;    // the workgroup's first token
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int head = wave & 3;
   const int64_t t0 = tb + 32 * (wave >> 2);                 // this wave's first token

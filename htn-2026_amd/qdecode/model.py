@@ -367,12 +367,14 @@ class BlockRunner:
             pass
 
 
-# Rows per causal prefill forward.  6144 = 24 blocks of the prefill GEMM's 256-row tiles, so the
-# o / down projections (10 blocks of 256 weight rows) fill 240 of the 256 CUs in one round.
-# Measured on MI355X (prefill + first token): 4 x 8192 0.395-0.398 s (4096 rows: 0.408, 5120:
-# 0.399, 7168: 0.430, 8192: 0.418, 12288: 0.404, 16384: 0.441); 32 x 2048 0.560 s (4096: 0.614,
-# 5120: 0.564, 7168: 0.658, 8192: 0.606, 12288: 0.548, 16384: 0.565).
-PREFILL_ROWS = 6144
+# Rows per causal prefill forward.  32768 = 128 blocks of the prefill GEMM's 256-row tiles: every
+# projection's tile grid is a whole number of rounds over 256 CUs (qkv 3072 tiles, o / down 1280,
+# gate/up 9728), and four prompts of 8192 tokens go through in one chunk.
+# Measured on MI355X (prefill + first token, second of three runs): 4 x 8192 0.330 s (6144 rows:
+# 0.342, 8192: 0.356, 12288: 0.335, 16384: 0.330, 24576: 0.336); 32 x 2048 0.515 s (6144: 0.541,
+# 8192: 0.578, 12288: 0.521, 16384: 0.527, 24576: 0.524).  The block step's buffers grow with it
+# (about 1.7 GB of activations at 32768 rows).
+PREFILL_ROWS = 32768
 
 
 def prefill_chunk(B, S, budget_rows=PREFILL_ROWS):
