@@ -48,10 +48,10 @@ PEAK_HBM_GBS = 8000.0
 # factors being what the same counters read for a 512 MiB device copy.  Summary and commands:
 # profiles/gemv_gate_up_b1_traffic.md.
 GU_TRAFFIC_B1 = 99_775_769
-# HBM bytes per persistent-step launch at B=1 (config 3), same method (FETCH_SIZE 4,002,957.0
-# KiB x 1.99986 + WRITE_SIZE 27,300.1 KiB), mean over the profiled steps at positions 512..520;
+# HBM bytes per persistent-step launch at B=1 (config 3), same method (FETCH_SIZE 4,001,519.25
+# KiB x 1.99983 + WRITE_SIZE 19,108.1 KiB), mean over the profiled steps at positions 512..520;
 # summary and commands: profiles/mega_step_b1_traffic.md.
-MEGA_TRAFFIC_B1 = 8_225_445_228
+MEGA_TRAFFIC_B1 = 8_213_971_655
 METRIC = "decode tok/s (Qwen3-4B bf16, B=1 & B=32) + achieved HBM GB/s vs peak"
 
 
