@@ -59,6 +59,35 @@ class _Shape:
         self.err_host = torch.zeros((max(N, 1),), dtype=torch.int32, pin_memory=True)
         self.events = [torch.cuda.Event() for _ in range(max(N, 1))]
         self.graph_ready = False
+        self._tree_pass = None
+
+    def start(self, ids, decode_next=False):
+        """Enqueue the prompt (one host-to-device copy), its causal prefill and the first
+        token's readback into host row 0 (``events[0]`` marks it); with ``decode_next`` also set
+        pos = S and record the decode-step graph (once per shape).  Does not wait."""
+        with torch.cuda.stream(self.stream):
+            self.ids_host.copy_(ids)
+            self.ids.copy_(self.ids_host, non_blocking=True)
+            self.run_prefill()
+            self.host[0].copy_(self.kv.tok, non_blocking=True)
+            self.events[0].record(self.stream)
+            if decode_next:
+                self.kv.pos.fill_(self.S)
+                if not self.graph_ready:
+                    # the step reads tok/pos from the device; capture once per shape
+                    self.decode.capture()
+                    self.graph_ready = True
+
+    def first_token(self):
+        """Wait for the prefill's token (enqueued by ``start``) and return it (B ids)."""
+        self.events[0].synchronize()
+        return self.host[0].tolist()
+
+    def tree_pass(self):
+        """The tree runner's host twin (created on first use)."""
+        if self._tree_pass is None:
+            self._tree_pass = _tree.TreePass(self.tree, self.stream)
+        return self._tree_pass
 
     def run_prefill(self):
         """Causal chunks of the prompt: KV [0, S) and the first greedy token into kv.tok."""
@@ -205,18 +234,7 @@ class Engine:
     def _stream_plain(self, sh, ids, N):
         """Prefill, then N-1 graph replays of the decode step; the host yields step t-1 while
         the device runs step t (engine.py:719-757)."""
-        S = sh.S
-        with torch.cuda.stream(self.stream):
-            sh.ids_host.copy_(ids)
-            sh.ids.copy_(sh.ids_host, non_blocking=True)
-            sh.run_prefill()
-            sh.kv.pos.fill_(S)
-            sh.host[0].copy_(sh.kv.tok, non_blocking=True)
-            sh.events[0].record(self.stream)
-            if N > 1 and not sh.graph_ready:
-                # the step reads tok/pos from the device; capture once per shape
-                sh.decode.capture()
-                sh.graph_ready = True
+        sh.start(ids, decode_next=N > 1)
         err = sh.decode.err_word
         for t in range(1, N):
             with torch.cuda.stream(self.stream):

@@ -22,6 +22,7 @@ import torch
 
 from . import _lib, ops
 from .checkpoint import SafeTensors, read_config
+from .inputs import BlockInputs
 
 BF16 = torch.bfloat16
 
@@ -298,13 +299,12 @@ class BlockRunner:
         self.qkv = e(M, (m.Hq + 2 * m.Hkv) * 128)
         self.q, self.attn = e(M, m.Hq * 128), e(M, m.Hq * 128)
         self.act = e(M, m.I)
-        z = lambda *s, dt=torch.int64: torch.zeros(s, dtype=dt, device=dev)  # noqa: E731
-        self.tokens = z(B, t_max)
-        self.base = z(B)
-        self.depth = z(B, t_max)
-        self.anc = z(B, t_max)                     # uint64 masks stored in int64
-        self.c_base, self.c_src, self.c_cnt = z(B), z(B, t_max, dt=torch.int32), z(B, dt=torch.int32)
-        self.out_tok = z(M if lm_mode == _lib.LM_ALL else B)
+        self.inputs = BlockInputs(B, t_max, device=dev)
+        inp = self.inputs
+        self.tokens, self.base, self.depth, self.anc = inp.tokens, inp.base, inp.depth, inp.anc
+        self.c_base, self.c_src, self.c_cnt = inp.c_base, inp.c_src, inp.c_cnt
+        self.out_tok = torch.zeros((M if lm_mode == _lib.LM_ALL else B,), dtype=torch.int64,
+                                   device=dev)
         nbytes = _lib.LIB.qd_block_workspace_bytes(C.byref(m.qd), B, t_max, kv.cap)
         self.ws = torch.zeros((nbytes,), dtype=torch.uint8, device=dev)
         # hipGraphs of the forward, one per (T, compact, lm_mode): the forward reads every input

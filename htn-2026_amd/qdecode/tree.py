@@ -1,13 +1,15 @@
 """Host side of exact token-tree speculative decoding.
 
-Restates the reference's ``Tree`` and greedy accept walk (engine/spec.py:18-55, 124-150) and
-its verify loop (engine/engine.py:830-908) with two MI355X-side changes:
-  * the ancestor-or-self mask is 64 bits wide (the reference's int32 caps trees at 32 nodes,
-    engine.py:166-169), so a 64-node tree verifies in one block forward;
-  * draft sources are pluggable: ``random_tree_drafter`` builds the benchmark's uniformly
-    random 4-4-2-2 trees; ``draft.LookaheadDrafter`` restates the reference's window / n-gram
-    / prediction-pool sources (a stateful drafter: ``rows(seqs)`` gives per-sequence sources
-    that draft a tree, observe the verified argmaxes and index the emitted text).
+``Tree`` and the greedy accept walk restate the reference's tree encoding and walk
+(engine/spec.py:18-55, 124-150): they define which ids are emitted.  The mask is 64 bits wide
+(the reference's int32 caps trees at 32 nodes, engine.py:166-169), so a 64-node tree verifies
+in one block forward.  The verification loop (``stream_tree``, the counterpart of the
+reference's engine.py:830-908) is built around per-sequence ``RowState`` objects and one
+pinned input block per forward (``TreePass``).  Draft sources are pluggable:
+``random_tree_drafter`` builds the benchmark's uniformly random 4-4-2-2 trees;
+``draft.LookaheadDrafter`` restates the reference's window / n-gram / prediction-pool sources
+(a stateful drafter: ``rows(seqs)`` gives per-sequence sources that draft a tree, observe the
+verified argmaxes and index the emitted text).
 
 Node 0 is the last emitted token (its K/V is not cached yet); parents precede children, so
 node index >= depth.  Node i is rotated at base + depth_i, written to cache slot base + i,
@@ -16,8 +18,12 @@ accepted path (root, n_1, .., n_a) is compacted to slots base .. base + a by the
 forward (qd_kv_compact), and the emitted tokens are exactly the model's greedy choices.
 """
 
+import time
+
 import numpy as np
 import torch
+
+from .inputs import BlockInputs
 
 
 class Tree:
@@ -110,89 +116,157 @@ def branching_tree(root, T, branching, draw):
 
 def random_tree_drafter(seed, vocab=151936, branching=(4, 4, 2, 2)):
     """The benchmark's draft source: uniformly random ids in a 4-4-2-2 tree (root + the first
-    T-1 BFS nodes of the 117-node tree)."""
+    T-1 BFS nodes of the 117-node tree).  The ids of one tree are drawn in a single call."""
     rng = np.random.default_rng(seed)
+    full = 1
+    width = 1
+    for fan in branching:
+        width *= fan
+        full += width
 
     def drafter(seq, T):
-        return branching_tree(seq[-1], T, branching, lambda n: rng.integers(0, vocab, size=n))
+        ids = iter(rng.integers(0, vocab, size=full).tolist())
+        return branching_tree(seq[-1], T, branching, lambda n: [next(ids) for _ in range(n)])
     return drafter
 
 
+# ----------------------------------------------------------------------------------------------
+# The verification loop.  Its state is per sequence (``RowState``: text, draft source, the tree
+# in flight, the cache slot of its root and the compaction that the next forward applies); the
+# device side is one BlockRunner and a pinned twin of its input block (``TreePass``), so every
+# pass moves all inputs host -> device in one copy and all argmaxes back in one copy.
+# ----------------------------------------------------------------------------------------------
+
+class _FnSource:
+    """A plain ``drafter(text, T) -> Tree`` seen as a per-sequence source with no state."""
+
+    def __init__(self, fn, text):
+        self.fn, self.text = fn, text
+
+    def draft(self, T, depth):
+        return self.fn(self.text, T)
+
+    def observe(self, tree, g, path):
+        pass
+
+    def index(self):
+        pass
+
+
+class RowState:
+    """One sequence under tree verification.
+
+    ``text`` is prompt + emitted ids (shared with the draft source); ``slot`` is the cache slot
+    of the next tree's node 0, which is always the last emitted id, so slot = len(text) - 1;
+    ``moves`` = (slot of the verified tree, its accepted node indices) is the compaction that
+    the next forward performs first (node k of the accepted path goes to slot + k)."""
+
+    __slots__ = ("text", "n_prompt", "source", "tree", "slot", "moves")
+
+    def __init__(self, text, n_prompt, source):
+        self.text, self.n_prompt, self.source = text, n_prompt, source
+        self.tree = None
+        self.slot = len(text) - 1
+        self.moves = (self.slot, [0])            # identity until a tree has been verified
+
+    @property
+    def emitted(self):
+        return len(self.text) - self.n_prompt
+
+    def stage(self, arr, b, T, depth):
+        """Draft this pass's tree and write it, its slot and the pending compaction into row b
+        of the host input arrays (``BlockInputs.arrays()`` of the pinned twin)."""
+        tree = self.source.draft(T, depth)
+        if len(tree.tokens) != T:
+            raise ValueError(f"draft tree has {len(tree.tokens)} nodes, the forward takes {T}")
+        self.tree = tree
+        arr["tokens"][b] = tree.tokens
+        arr["depth"][b] = tree.depth
+        arr["anc"][b] = np.array(tree.anc, dtype=np.uint64).view(np.int64)
+        arr["base"][b] = self.slot
+        at, nodes = self.moves
+        arr["c_base"][b] = at
+        arr["c_src"][b, :len(nodes)] = nodes
+        arr["c_src"][b, len(nodes):] = 0
+        arr["c_cnt"][b] = len(nodes)
+
+    def settle(self, g):
+        """Take the model's argmax after every node of the tree in flight (``g``, T ids):
+        append the accepted ids to the text and plan their compaction.  Returns how many ids
+        this pass emitted for the sequence."""
+        out, path = accept(self.tree, g)
+        self.source.observe(self.tree, g, path)
+        self.moves = (self.slot, [0] + path)
+        self.text.extend(out)
+        self.source.index()
+        self.slot = len(self.text) - 1
+        return len(out)
+
+
+class TreePass:
+    """One tree-verification forward per call: the pinned input twin of ``runner`` is copied to
+    the device in one transfer, the forward (compaction first) is replayed, and the per-node
+    argmaxes come back in one transfer; ``run()`` returns them as a [B, T] numpy array."""
+
+    def __init__(self, runner, stream):
+        self.runner, self.stream = runner, stream
+        B, T = runner.kv.B, runner.t_max
+        self.B, self.T = B, T
+        self.host = BlockInputs(B, T, pinned=True)
+        self.arrays = self.host.arrays()
+        self.out = torch.empty((B * T,), dtype=torch.int64, pin_memory=True)
+        self.out_np = self.out.numpy().reshape(B, T)
+        self.done = torch.cuda.Event()
+
+    def run(self):
+        with torch.cuda.stream(self.stream):
+            self.runner.inputs.block.copy_(self.host.block, non_blocking=True)
+            self.runner.launch(self.T, compact=True)
+            self.out.copy_(self.runner.out_tok, non_blocking=True)
+            self.done.record(self.stream)
+        self.done.synchronize()
+        return self.out_np
+
+
 def stream_tree(engine, sh, ids, N, drafter):
-    """Prefill, then verify one draft tree per sequence per block forward until every row has
-    N tokens; yields exactly N lists of B ids (engine.py:830-908)."""
+    """Prefill, then one verification forward of a T-node draft tree per sequence per pass
+    until every sequence has N ids; yields exactly N lists of B ids, each column as soon as
+    every sequence has it (the reference's loop: engine/engine.py:830-908).
+
+    A sequence that already has N ids is not staged again: its row of the input block keeps
+    the last tree it verified, at the same slots (all inside its cache), and its outputs are
+    ignored -- its cache is no longer read.  ``engine.tree_stats`` records the passes, the ids
+    each sequence took per pass and the host time per pass (staging + accept walks)."""
     B, S, T = sh.B, sh.S, sh.tree_T
-    tr = sh.tree
-    stream = engine.stream
-    with torch.cuda.stream(stream):
-        sh.ids_host.copy_(ids)
-        sh.ids.copy_(sh.ids_host, non_blocking=True)
-        sh.run_prefill()
-        sh.host[0].copy_(sh.kv.tok, non_blocking=True)
-        sh.events[0].record(stream)
-    sh.events[0].synchronize()
-    first = sh.host[0].tolist()
+    sh.start(ids)
+    first = sh.first_token()
     yield first
     if N == 1:
         return
-    seqs = [list(map(int, r)) + [t] for r, t in zip(ids.tolist(), first)]
-    rows = drafter.rows(seqs) if hasattr(drafter, "rows") else None
+    texts = [list(map(int, r)) + [t] for r, t in zip(ids.tolist(), first)]
+    if hasattr(drafter, "rows"):
+        sources = drafter.rows(texts)
+    else:
+        sources = [_FnSource(drafter, tx) for tx in texts]
+    rows = [RowState(tx, S, src) for tx, src in zip(texts, sources)]
     depth = min(T - 1, getattr(drafter, "max_depth", T - 1))
-    c_base, c_src, c_cnt = [S] * B, [[0] * T for _ in range(B)], [1] * B
-    pin = lambda shape, dt: torch.empty(shape, dtype=dt, pin_memory=True)  # noqa: E731
-    h_tok, h_depth, h_anc = pin((B, T), torch.int64), pin((B, T), torch.int64), pin((B, T), torch.int64)
-    h_base, h_cb, h_cs, h_cc = pin((B,), torch.int64), pin((B,), torch.int64), pin((B, T), torch.int32), pin((B,), torch.int32)
-    h_out = pin((B * T,), torch.int64)
-    ev = torch.cuda.Event()
-    yielded = 1
-    stats = {"passes": 0, "accepted": []}
-    while yielded < N:
+    tp = sh.tree_pass()
+    stats = {"passes": 0, "accepted": [], "host_ms": []}
+    sent = 1
+    while sent < N:
+        t0 = time.perf_counter()
+        live = [b for b in range(B) if rows[b].emitted < N]
+        for b in live:
+            rows[b].stage(tp.arrays, b, T, depth)
+        t1 = time.perf_counter()
+        g = tp.run()
+        t2 = time.perf_counter()
+        for b in live:
+            stats["accepted"].append(rows[b].settle(g[b].tolist()))
         stats["passes"] += 1
-        trees, bases = [], []
-        for b in range(B):
-            sq = seqs[b]
-            if len(sq) - S >= N:                 # done: verify an inert tree at a safe slot
-                tree = Tree(sq[-1])
-                tree.pad(T)
-                trees.append(None)
-                bases.append(S)
-            else:
-                tree = rows[b].draft(T, depth) if rows else drafter(sq, T)
-                trees.append(tree)
-                bases.append(len(sq) - 1)
-            h_tok[b] = torch.tensor(tree.tokens, dtype=torch.int64)
-            h_depth[b] = torch.tensor(tree.depth, dtype=torch.int64)
-            h_anc[b] = torch.tensor(tree.anc_i64(), dtype=torch.int64)
-        h_base.copy_(torch.tensor(bases, dtype=torch.int64))
-        h_cb.copy_(torch.tensor(c_base, dtype=torch.int64))
-        h_cs.copy_(torch.tensor(c_src, dtype=torch.int32))
-        h_cc.copy_(torch.tensor(c_cnt, dtype=torch.int32))
-        with torch.cuda.stream(stream):
-            for d, h in ((tr.tokens, h_tok), (tr.depth, h_depth), (tr.anc, h_anc), (tr.base, h_base),
-                         (tr.c_base, h_cb), (tr.c_src, h_cs), (tr.c_cnt, h_cc)):
-                d.copy_(h, non_blocking=True)
-            tr.launch(T, compact=True)
-            h_out.copy_(tr.out_tok, non_blocking=True)
-            ev.record(stream)
-        ev.synchronize()
-        g = h_out.tolist()
-        for b in range(B):
-            tree = trees[b]
-            if tree is None:
-                c_cnt[b] = 1
-                continue
-            gb = g[b * T:(b + 1) * T]
-            emitted, path = accept(tree, gb)
-            c_base[b] = bases[b]
-            c_src[b] = [0] + path + [0] * (T - 1 - len(path))
-            c_cnt[b] = len(path) + 1
-            if rows:
-                rows[b].observe(tree, gb, path)
-            seqs[b].extend(emitted)
-            if rows:
-                rows[b].index()
-            stats["accepted"].append(len(emitted))
-        while yielded < N and all(len(sq) - S > yielded for sq in seqs):
-            yield [sq[S + yielded] for sq in seqs]
-            yielded += 1
+        stats["host_ms"].append((t1 - t0 + time.perf_counter() - t2) * 1e3)
+        ready = min(N, min(r.emitted for r in rows))
+        for t in range(sent, ready):
+            yield [r.text[S + t] for r in rows]
+        sent = max(sent, ready)
     engine.tree_stats = stats
