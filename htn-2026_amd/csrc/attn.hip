@@ -566,19 +566,40 @@ static int64_t block_attn_cus() {
   return cus;
 }
 
-void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
-                       const int64_t* base, const uint64_t* anc, int64_t B, int64_t T, int Hq,
-                       int Hkv, int64_t cap, int64_t splits, float* ws_acc, float* ws_ml,
-                       bf16_t* out, hipStream_t s) {
-  if (B * T <= 0) return;
+int64_t block_attn_launch_splits(int64_t B, int64_t T, int Hkv, int64_t cap) {
   const int64_t QB = (T + BA_TQ - 1) / BA_TQ;
   const int64_t blocks = (int64_t)Hkv * B * QB;
-  int64_t use = block_attn_cus() / blocks;
-  if (use > splits) use = splits;
+  int64_t use = block_attn_cus() / (blocks > 0 ? blocks : 1);
+  const int64_t most = block_attn_splits(cap);
+  if (use > most) use = most;
   if (use < 1) use = 1;
   int64_t chunk = (cap + use - 1) / use;
   chunk = (chunk + 31) / 32 * 32;
-  use = (cap + chunk - 1) / chunk;                      // no empty trailing split
+  return (cap + chunk - 1) / chunk;                     // no empty trailing split
+}
+
+int64_t block_attn_partial_rows(int64_t B, int64_t T, int Hq, int Hkv, int64_t cap) {
+  // the split count is constant over the T of one query-block count and the rows grow with T,
+  // so the largest need of each query-block count sits at its largest T
+  int64_t most = 0;
+  const int64_t QB = (T + BA_TQ - 1) / BA_TQ;
+  for (int64_t qb = 1; qb <= QB; ++qb) {
+    const int64_t t = qb * BA_TQ < T ? qb * BA_TQ : T;
+    const int64_t use = block_attn_launch_splits(B, t, Hkv, cap);
+    const int64_t rows = use > 1 ? B * t * Hq * use : 0;
+    if (rows > most) most = rows;
+  }
+  return most;
+}
+
+void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
+                       const int64_t* base, const uint64_t* anc, int64_t B, int64_t T, int Hq,
+                       int Hkv, int64_t cap, float* ws_acc, float* ws_ml, bf16_t* out,
+                       hipStream_t s) {
+  if (B * T <= 0) return;
+  const int64_t QB = (T + BA_TQ - 1) / BA_TQ;
+  const int64_t use = block_attn_launch_splits(B, T, Hkv, cap);
+  const int64_t chunk = ((cap + use - 1) / use + 31) / 32 * 32;
   block_attn_mfma_kernel<<<dim3((unsigned)use, (unsigned)Hkv, (unsigned)(B * QB)), dim3(512), 0,
                            s>>>(q, k_cache, v_cache, base, anc, T, Hq, Hkv, cap, chunk,
                                 (1.0f / sqrtf(128.0f)) * 1.44269504088896341f, ws_acc, ws_ml,

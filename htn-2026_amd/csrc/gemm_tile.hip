@@ -1010,6 +1010,29 @@ static bool rows_plan(int64_t M, int64_t N, int64_t K, int epi, bool can_split, 
   return best.splits > 0;
 }
 
+// The block height (MFMA tiles) of the instantiation launch_rows picks for a plan: SwiGLU 2..5,
+// split-K 1..4, 6, 8, unsplit store / residual 1..4 (rows_plan's rounding and limits keep
+// 16 x this >= the plan's rows).
+static int rows_inst_nt(int nt, int epi, bool split) {
+  if (epi == EPI_SWIGLU) return nt <= 2 ? 2 : nt >= 5 ? 5 : nt;
+  if (split) return nt <= 1 ? 1 : nt <= 4 ? nt : nt <= 6 ? 6 : 8;
+  return nt <= 1 ? 1 : nt >= 4 ? 4 : nt;
+}
+
+// What the launchers run on the all-rows kernel for (M, N, K, epi) with `part_floats` floats of
+// split-partial room (0: none).  Returns -1 when the kernel does not take the shape (the tiled
+// kernels do), 0 when it does but the caller only takes split partials (gemm_tile_partials) and
+// no split fits, 1 with the plan to launch: split when the plan splits and the partials fit,
+// else the unsplit plan.
+static int rows_launch_plan(int64_t M, int64_t N, int64_t K, int epi, bool partials_only,
+                            int64_t part_floats, RowsPlan& P) {
+  if (M < GEMM_TILE_MIN_M || !rows_plan(M, N, K, epi, true, P)) return -1;
+  const bool room = part_floats >= (int64_t)P.splits * M * N;
+  if (partials_only) return P.splits > 1 && room ? 1 : 0;
+  if (P.splits > 1 && !room) rows_plan(M, N, K, epi, false, P);   // no room for partials: S = 1
+  return P.splits > 0 ? 1 : -1;
+}
+
 template <int EPI, bool SPLIT>
 static void launch_rows(const RowsPlan& P, const bf16_t* x, int64_t xs, int M, const bf16_t* w,
                         int N, int K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs,
@@ -1022,15 +1045,16 @@ static void launch_rows(const RowsPlan& P, const bf16_t* x, int64_t xs, int M, c
                                                        P.ks_per, P.mh, out, os, res, rs, part)
 #define QD_RW_MT(NT) \
   do { if (P.mt == 1) QD_RW(NT, 1); else QD_RW(NT, 2); } while (0)
+  const int nt = rows_inst_nt(P.nt, EPI, SPLIT);
   if constexpr (EPI == EPI_SWIGLU) {
-    switch (P.nt) {
+    switch (nt) {
       case 2: QD_RW_MT(2); break;
       case 3: QD_RW_MT(3); break;
       case 4: QD_RW_MT(4); break;
       default: QD_RW_MT(5); break;
     }
   } else if constexpr (SPLIT) {
-    switch (P.nt) {
+    switch (nt) {
       case 1: QD_RW_MT(1); break;
       case 2: QD_RW_MT(2); break;
       case 3: QD_RW_MT(3); break;
@@ -1039,7 +1063,7 @@ static void launch_rows(const RowsPlan& P, const bf16_t* x, int64_t xs, int M, c
       default: QD_RW_MT(8); break;
     }
   } else {
-    switch (P.nt) {
+    switch (nt) {
       case 1: QD_RW_MT(1); break;
       case 2: QD_RW_MT(2); break;
       case 3: QD_RW_MT(3); break;
@@ -1048,6 +1072,26 @@ static void launch_rows(const RowsPlan& P, const bf16_t* x, int64_t xs, int M, c
   }
 #undef QD_RW_MT
 #undef QD_RW
+}
+
+int gemm_rows_query(int64_t M, int64_t N, int64_t K, int epi, bool partials_only,
+                    int64_t part_floats, int64_t* out) {
+  RowsPlan P;
+  const int rp = rows_launch_plan(M, N, K, epi, partials_only, part_floats, P);
+  if (rp != 1) return rp;
+  const bool split = P.splits > 1;
+  const int nt = rows_inst_nt(P.nt, split ? EPI_NONE : epi, split);
+  const int64_t nblk = (N + P.rows - 1) / P.rows * P.splits;
+  const int wt = (!split && epi == EPI_SWIGLU) ? 2 * nt : nt;
+  out[0] = P.rows;
+  out[1] = nt;
+  out[2] = P.mt;
+  out[3] = P.mh;
+  out[4] = P.splits;
+  out[5] = P.ks_per;
+  out[6] = P.mh > 1 ? (nblk + 7) / 8 * 8 * P.mh : nblk;             // grid (launch_rows)
+  out[7] = (int64_t)RW_NBUF * (16 * wt + 128 * P.mt) * 128;          // static LDS bytes
+  return 1;
 }
 
 int64_t gemm_tile_ws_floats(int64_t M, int64_t N, int64_t K, int epi) {
@@ -1064,8 +1108,9 @@ int gemm_tile_partials(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, 
       !gemm_tile_ok(M, N, K, EPI_NONE, x, xs, w, part, N, nullptr, 0))
     return 0;
   RowsPlan P;
-  if (rows_plan(M, N, K, EPI_NONE, true, P)) {
-    if (P.splits <= 1 || part_floats < (int64_t)P.splits * M * N) return 0;
+  const int rp = rows_launch_plan(M, N, K, EPI_NONE, true, part_floats, P);
+  if (rp == 0) return 0;
+  if (rp == 1) {
     launch_rows<EPI_NONE, true>(P, x, xs, (int)M, w, (int)N, (int)K, nullptr, 0, nullptr, 0,
                                 part, s);
     return P.splits;
@@ -1116,11 +1161,8 @@ int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w
         logits);
     return nbl;
   }
-  if (epi != EPI_ARGMAX) {
-    RowsPlan P;
-    if (rows_plan(M, N, K, epi, true, P) && P.splits > 1 &&
-        (!part || part_floats < (int64_t)P.splits * M * N))
-      rows_plan(M, N, K, epi, false, P);                      // no room for partials: S = 1
+  RowsPlan P;
+  if (epi != EPI_ARGMAX && rows_launch_plan(M, N, K, epi, false, part ? part_floats : 0, P) == 1) {
     if (P.splits > 1) {
       launch_rows<EPI_NONE, true>(P, x, xs, (int)M, w, (int)N, (int)K, nullptr, 0, nullptr, 0,
                                   part, s);
@@ -1132,15 +1174,13 @@ int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w
         gemm_split_reduce_kernel<EPI_NONE><<<rg, rb, 0, s>>>(part, P.splits, M, N, out, os, res, rs);
       return 0;
     }
-    if (P.splits == 1) {
-      if (epi == EPI_RES)
-        launch_rows<EPI_RES, false>(P, x, xs, (int)M, w, (int)N, (int)K, out, os, res, rs, part, s);
-      else if (epi == EPI_SWIGLU)
-        launch_rows<EPI_SWIGLU, false>(P, x, xs, (int)M, w, (int)N, (int)K, out, os, res, rs, part, s);
-      else
-        launch_rows<EPI_NONE, false>(P, x, xs, (int)M, w, (int)N, (int)K, out, os, res, rs, part, s);
-      return 0;
-    }
+    if (epi == EPI_RES)
+      launch_rows<EPI_RES, false>(P, x, xs, (int)M, w, (int)N, (int)K, out, os, res, rs, part, s);
+    else if (epi == EPI_SWIGLU)
+      launch_rows<EPI_SWIGLU, false>(P, x, xs, (int)M, w, (int)N, (int)K, out, os, res, rs, part, s);
+    else
+      launch_rows<EPI_NONE, false>(P, x, xs, (int)M, w, (int)N, (int)K, out, os, res, rs, part, s);
+    return 0;
   }
   const int64_t mblocks = (M + TM - 1) / TM, nblocks = tile_nblocks(N, epi);
   int splits = gemm_tile_splits(M, N, K, epi);

@@ -308,8 +308,8 @@ int qd_decode_attn(const uint16_t* qkv, int64_t qkv_stride, const uint16_t* q_no
 }
 
 int64_t qd_block_attn_workspace_bytes(int64_t batch, int64_t T, int64_t n_q_heads, int64_t cap) {
-  if (batch <= 0 || T <= 0 || cap <= 0) return 0;
-  const int64_t rows = batch * T * n_q_heads * block_attn_splits(cap);
+  if (batch <= 0 || T <= 0 || cap <= 0 || n_q_heads < 4) return 0;
+  const int64_t rows = block_attn_partial_rows(batch, T, (int)n_q_heads, (int)(n_q_heads / 4), cap);
   return align256(rows * 128 * 4) + align256(rows * 2 * 4);
 }
 
@@ -324,13 +324,12 @@ int qd_block_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_
   if (!q || !k_cache || !v_cache || !base || !out) return QD_EARG;
   if (!workspace || workspace_bytes < qd_block_attn_workspace_bytes(batch, T, n_q_heads, cap))
     return QD_EWS;
-  const int64_t splits = block_attn_splits(cap);
   Carver c(workspace);
-  const int64_t rows = batch * T * n_q_heads * splits;
+  const int64_t rows = block_attn_partial_rows(batch, T, (int)n_q_heads, (int)n_kv_heads, cap);
   float* acc = c.take<float>(rows * 128);
   float* ml = c.take<float>(rows * 2);
   launch_block_attn(q, k_cache, v_cache, base, anc, batch, T, (int)n_q_heads, (int)n_kv_heads, cap,
-                    splits, acc, ml, out, S(stream));
+                    acc, ml, out, S(stream));
   return launched();
 }
 
@@ -631,19 +630,24 @@ static int64_t block_part_floats(const qd_weights* w, int64_t M) {
   return f;
 }
 
-int64_t qd_block_workspace_bytes(const qd_weights* w, int64_t batch, int64_t T, int64_t cap) {
-  if (!w || batch <= 0 || T <= 0 || cap <= 0) return 0;
-  // LM region first, sized for either row count (all rows or the last row per sequence)
-  Carver a(nullptr), b(nullptr);
-  carve_lm(a, batch, w->vocab, w->hidden);
-  carve_lm(b, batch * T, w->vocab, w->hidden);
+int64_t qd_block_workspace_bytes_lm(const qd_weights* w, int64_t batch, int64_t T, int64_t cap,
+                                    int32_t lm_mode) {
+  if (!w || batch <= 0 || T <= 0 || cap <= 0 || lm_mode < QD_LM_ALL || lm_mode > QD_LM_NONE)
+    return 0;
+  // LM-head region first: partials for every row (QD_LM_ALL) or the last row per sequence
   Carver c(nullptr);
-  c.off = a.off > b.off ? a.off : b.off;
-  const int64_t rows = batch * T * w->n_q_heads * block_attn_splits(cap);
+  carve_lm(c, lm_mode == QD_LM_ALL ? batch * T : batch, w->vocab, w->hidden);
+  // attention split partials only for the row counts whose launches split the keys (a tree
+  // verification; a prefill chunk of >= 1024 rows runs one split and needs none)
+  const int64_t rows = block_attn_partial_rows(batch, T, w->n_q_heads, w->n_kv_heads, cap);
   c.take<float>(rows * 128);
   c.take<float>(rows * 2);
   c.take<float>(block_part_floats(w, batch * T));
   return c.off;
+}
+
+int64_t qd_block_workspace_bytes(const qd_weights* w, int64_t batch, int64_t T, int64_t cap) {
+  return qd_block_workspace_bytes_lm(w, batch, T, cap, QD_LM_ALL);   // enough for every mode
 }
 
 int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
@@ -657,14 +661,14 @@ int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
     return QD_EARG;
   if (!st->causal && (!st->anc || !st->depth || T > 64)) return QD_EARG;
   if (block_attn_splits(cap) > 1024) return QD_EARG;
-  if (!st->workspace || st->workspace_bytes < qd_block_workspace_bytes(w, B, T, cap)) return QD_EWS;
+  if (!st->workspace || st->workspace_bytes < qd_block_workspace_bytes_lm(w, B, T, cap, st->lm_mode))
+    return QD_EWS;
   hipStream_t s = S(stream);
   const int64_t M = B * T;
-  const int64_t splits = block_attn_splits(cap);
   Carver c(st->workspace);
   const int64_t lm_rows = st->lm_mode == QD_LM_ALL ? M : B;
   LmWs lw = carve_lm(c, lm_rows, V, H);
-  const int64_t arows = M * Hq * splits;
+  const int64_t arows = block_attn_partial_rows(B, T, Hq, Hkv, cap);
   float* acc = c.take<float>(arows * 128);
   float* ml = c.take<float>(arows * 2);
   const int64_t part_floats = block_part_floats(w, M);
@@ -702,7 +706,7 @@ int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
                           st->q, kc, vc, B, T, Hq, Hkv, cap, w->eps, s);
     }
     launch_block_attn(st->q, kc, vc, st->base, st->causal ? nullptr : st->anc, B, T, Hq, Hkv, cap,
-                      splits, acc, ml, st->attn, s);
+                      acc, ml, st->attn, s);
     const int so = gemm_tile_partials(st->attn, QD, M, w->w_o + l * H * QD, H, QD, part,
                                       part_floats, s);
     if (so) {
@@ -733,6 +737,14 @@ int qd_block_step(const qd_weights* w, const qd_block_state* st, void* stream) {
                    st->out_tok, nullptr, nullptr, lw, s);
   return lm_head(st->x, H, lm_weight(w), V, H, M, w->final_norm, w->eps, st->out_tok, nullptr, nullptr,
                  lw, s);
+}
+
+// ------------------------------------------------------------------ plan queries (host only)
+int qd_gemm_rows_plan(int64_t M, int64_t N, int64_t K, int32_t epi, int64_t part_floats,
+                      int32_t partials_only, int64_t* out) {
+  if (!out || M <= 0 || N <= 0 || K <= 0 || epi < EPI_NONE || epi > EPI_SWIGLU) return QD_EARG;
+  if (epi == EPI_SWIGLU && partials_only) return QD_EARG;
+  return gemm_rows_query(M, N, K, epi, partials_only != 0, part_floats, out);
 }
 
 // ------------------------------------------------------------------ graphs

@@ -87,6 +87,11 @@ bool gemm_tile_ok(int64_t M, int64_t N, int64_t K, int epi, const void* x, int64
                   const void* w, const void* out, int64_t out_stride, const void* res,
                   int64_t res_stride);
 int gemm_tile_splits(int64_t M, int64_t N, int64_t K, int epi);
+// The all-rows kernel's launch for a shape (qd_gemm_rows_plan): -1 / 0 / 1 as rows_launch_plan;
+// with 1, out[8] = rows per workgroup, instantiated block height (MFMA tiles), activation
+// tiles per wave, activation halves, K splits, K steps per split, grid, static LDS bytes.
+int gemm_rows_query(int64_t M, int64_t N, int64_t K, int epi, bool partials_only,
+                    int64_t part_floats, int64_t* out);
 int64_t gemm_tile_ws_floats(int64_t M, int64_t N, int64_t K, int epi);
 int64_t launch_gemm_tile(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
                          int64_t K, bf16_t* out, int64_t os, const bf16_t* res, int64_t rs, int epi,
@@ -155,8 +160,16 @@ void launch_decode_attn_part(const float* part, int part_S, const bf16_t* qn, co
                              bf16_t* k_cache, bf16_t* v_cache, int64_t B, int Hq, int Hkv,
                              int64_t cap, int64_t splits, float eps, float* ws_acc, float* ws_ml,
                              bf16_t* out, bool rope_row, hipStream_t s);
+// Block attention (tree verification, causal prefill chunks).  Keys split into at most
+// block_attn_splits(cap) ranges; a launch of B x T query rows uses block_attn_launch_splits(),
+// as many as fit one round of workgroups over the CUs.  With more than one split it writes
+// fp32 partials (128 + 2 floats per query-head row and split) and merges them;
+// block_attn_partial_rows() is the number of partial rows any launch with T' <= T needs
+// (0 when all of them run one split and write their output directly).
 int64_t block_attn_splits(int64_t cap);
+int64_t block_attn_launch_splits(int64_t B, int64_t T, int Hkv, int64_t cap);
+int64_t block_attn_partial_rows(int64_t B, int64_t T, int Hq, int Hkv, int64_t cap);
 void launch_block_attn(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
                        const int64_t* base, const uint64_t* anc, int64_t B, int64_t T, int Hq,
-                       int Hkv, int64_t cap, int64_t splits, float* ws_acc, float* ws_ml,
-                       bf16_t* out, hipStream_t s);
+                       int Hkv, int64_t cap, float* ws_acc, float* ws_ml, bf16_t* out,
+                       hipStream_t s);

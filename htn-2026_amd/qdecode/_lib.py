@@ -83,7 +83,9 @@ SIGNATURES = {
     "qd_mega_ctl_offset": ([C.POINTER(Weights), i64, i64], i64),
     "qd_mega_step": ([C.POINTER(Weights), C.POINTER(DecodeState), p], i32),
     "qd_block_workspace_bytes": ([C.POINTER(Weights), i64, i64, i64], i64),
+    "qd_block_workspace_bytes_lm": ([C.POINTER(Weights), i64, i64, i64, i32], i64),
     "qd_block_step": ([C.POINTER(Weights), C.POINTER(BlockState), p], i32),
+    "qd_gemm_rows_plan": ([i64, i64, i64, i32, i64, i32, C.POINTER(i64)], i32),
     "qd_graph_begin": ([p], i32),
     "qd_graph_end": ([p, C.POINTER(C.c_void_p)], i32),
     "qd_graph_launch": ([p, p], i32),

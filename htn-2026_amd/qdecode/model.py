@@ -305,7 +305,9 @@ class BlockRunner:
         self.c_base, self.c_src, self.c_cnt = inp.c_base, inp.c_src, inp.c_cnt
         self.out_tok = torch.zeros((M if lm_mode == _lib.LM_ALL else B,), dtype=torch.int64,
                                    device=dev)
-        nbytes = _lib.LIB.qd_block_workspace_bytes(C.byref(m.qd), B, t_max, kv.cap)
+        # sized for the runner's own LM mode (a prefill runner ranks one row per sequence, or
+        # none) and every T <= t_max; a launch asking for more fails with QD_EWS
+        nbytes = _lib.LIB.qd_block_workspace_bytes_lm(C.byref(m.qd), B, t_max, kv.cap, lm_mode)
         self.ws = torch.zeros((nbytes,), dtype=torch.uint8, device=dev)
         # hipGraphs of the forward, one per (T, compact, lm_mode): the forward reads every input
         # (tokens, base, depth, anc, compaction lists) from these device buffers, so a replay
@@ -373,7 +375,7 @@ class BlockRunner:
 # Measured on MI355X (prefill + first token, second of three runs): 4 x 8192 0.330 s (6144 rows:
 # 0.342, 8192: 0.356, 12288: 0.335, 16384: 0.330, 24576: 0.336); 32 x 2048 0.515 s (6144: 0.541,
 # 8192: 0.578, 12288: 0.521, 16384: 0.527, 24576: 0.524).  The block step's buffers grow with it
-# (about 1.7 GB of activations at 32768 rows).
+# (1.91 GB of activations at 32768 rows; its workspace stays at ~34 MB whatever the context).
 PREFILL_ROWS = 32768
 
 

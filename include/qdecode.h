@@ -254,9 +254,29 @@ typedef struct {
 } qd_block_state;
 
 /* Replaces _verify_tree (engine/engine.py:445-461) and, as a causal chunk, the prompt
- * forward of _prefill (engine/engine.py:550-592). */
+ * forward of _prefill (engine/engine.py:550-592).
+ * Workspace: qd_block_workspace_bytes_lm() is what a step with this lm_mode and any T' <= T
+ * needs (the LM head's partials for batch * T rows with QD_LM_ALL, for batch rows otherwise;
+ * attention split partials only where the launch splits the keys, which does not grow with
+ * cap; the projections' split-K partials); qd_block_workspace_bytes() is the QD_LM_ALL size,
+ * enough for every mode.  Both depend on the current device's CU count (256 assumed when no
+ * device is visible). */
 int64_t qd_block_workspace_bytes(const qd_weights *w, int64_t batch, int64_t T, int64_t cap);
+int64_t qd_block_workspace_bytes_lm(const qd_weights *w, int64_t batch, int64_t T, int64_t cap,
+                                    int32_t lm_mode);
 int qd_block_step(const qd_weights *w, const qd_block_state *st, void *stream);
+
+/* Host-only plan query of the all-rows projection kernel (65..256 activation rows, the
+ * tree-verification GEMMs): what qd_linear / qd_block_step launch for an M x K by N x K
+ * product with epilogue `epi` (QD_EPI_NONE / RES / SWIGLU) and `part_floats` floats of room for
+ * fp32 split-K partials (partials_only != 0: the block step's partial-summing consumers, which
+ * launch nothing unless the plan splits).  Returns -1 when another kernel serves the shape, 0
+ * when partials_only finds no split, 1 with out[8] = {rows per workgroup, block height in MFMA
+ * tiles, activation tiles per wave, activation halves, K splits, K steps per split, grid, static
+ * LDS bytes}; QD_EARG for bad arguments.  No reference counterpart: the CPU tests use it to
+ * check every plan's grid coverage and store bounds without a GPU. */
+int qd_gemm_rows_plan(int64_t M, int64_t N, int64_t K, int32_t epi, int64_t part_floats,
+                      int32_t partials_only, int64_t *out);
 
 /* hipGraph capture of whatever is enqueued on `stream` between begin and end (replaces the
  * torch.cuda.CUDAGraph capture of the decode step, engine/engine.py:685-713). */

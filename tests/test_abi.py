@@ -84,6 +84,32 @@ def test_workspace_sizes(lib):
     assert L.qd_decode_step(C.byref(bad), C.byref(st), None) == lib.QD_EARG
 
 
+def test_block_workspace_sizes(lib):
+    """The block step's workspace at the benchmark shapes (no device here: 256 CUs assumed).
+    Attention split partials exist only where the launch splits the keys and never grow with
+    the context; a prefill runner (QD_LM_LAST) reserves LM-head room for one row per sequence."""
+    L = lib.LIB
+    w = lib.Weights(36, 2560, 9728, 151936, 32, 8, 128, 1e-6, *([256] * 10))
+    al = lambda n: (n + 255) // 256 * 256                                       # noqa: E731
+    # config-5 verify: 4 sequences x 8 KV heads x 1 query block = 32 workgroups per key split,
+    # so 256 / 32 = 8 splits; 4 * 64 rows * 32 heads * 8 splits partial rows of 128 + 2 floats
+    rows = 4 * 64 * 32 * 8
+    assert L.qd_block_attn_workspace_bytes(4, 64, 32, 8512) == al(rows * 512) + al(rows * 8)
+    # prefill chunks of 32768 rows: >= 256 workgroups with one split, no partials at any context
+    for cap in (2176, 8512, 131328):
+        assert L.qd_block_attn_workspace_bytes(32, 1024, 32, cap) == 0
+    verify = L.qd_block_workspace_bytes_lm(C.byref(w), 4, 64, 8512, lib.LM_ALL)
+    assert verify == L.qd_block_workspace_bytes(C.byref(w), 4, 64, 8512) < 100 << 20
+    for B, T in ((4, 8192), (32, 1024), (1, 32768), (8, 4096)):
+        sizes = [L.qd_block_workspace_bytes_lm(C.byref(w), B, T, cap, lib.LM_LAST)
+                 for cap in (T + 256, 32768 + 256, 131072 + 256)]
+        assert sizes[0] == sizes[1] == sizes[2] < 64 << 20, (B, T, sizes)
+        none = L.qd_block_workspace_bytes_lm(C.byref(w), B, T, T + 256, lib.LM_NONE)
+        every = L.qd_block_workspace_bytes_lm(C.byref(w), B, T, T + 256, lib.LM_ALL)
+        assert none <= sizes[0] < every
+    assert L.qd_block_workspace_bytes_lm(C.byref(w), 4, 64, 8512, 3) == 0              # bad mode
+
+
 def test_missing_library_raises(tmp_path):
     """The product path has no fallback: a missing library is an ImportError."""
     import subprocess
