@@ -471,7 +471,7 @@ def cpu_baseline(budget_s=15.0, prompt_len=512):
         lg = ref.prefill(prompt, cache)
         tok = qwen3_ref.argmax_lowest(lg[:, -1])
         n, t1 = 0, time.perf_counter()
-        while n < 3 or (time.perf_counter() - t1 < budget_s and n < 60):
+        while n < 3 or (time.perf_counter() - t1 < budget_s and n < 400):
             lg = ref.decode(tok, prompt_len + n, cache)
             tok = qwen3_ref.argmax_lowest(lg)
             n += 1

@@ -187,7 +187,9 @@ int qd_decode_step(const qd_weights *w, const qd_decode_state *st, void *stream)
  * of QD_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends); st->workspace and
  * st->workspace_bytes are ignored.  Same kernels and results as qd_decode_step (bit-identical).
  * Returns QD_ESCRATCH, before touching the device, when qd_decode_workspace_bytes(w, batch, cap)
- * exceeds the array (at Qwen3-4B's shape batch 32 fits up to cap 94208, batch 64 up to 40960).
+ * exceeds the array (at Qwen3-4B's shape batch 32 fits up to cap 106496, batch 64 up to 40960).
+ * A first call under hipGraph capture (relaxed mode) resolves the array's address there and
+ * is supported.
  * The stream must belong to the current device.  Every call on one GPU shares that GPU's
  * array, whose contents the next call overwrites: calls that overlap on one GPU
  * (different streams, or host threads) race and must be serialised by the caller.  Allocates

@@ -9,7 +9,10 @@ Both run one causal forward over the config-3 prompt and the stored oracle run's
 (depth.json: 36 layers, seed 1, prompt seed 301, 512 ids + 31 greedy tokens) and are compared
 at every position: how much the top-2 gap moves between them, where their argmax differs, and
 B's argmax deficit under A -- how far below A's argmax the token that a valid implementation
-picks can sit.
+picks can sit -- and the largest logit difference over the whole vocabulary at each position.
+Variant C adds the other reordering a kernel implementation makes: every projection (and the
+LM head) summed as fp32 partials over 512-wide K ranges.  ``logit_floor`` is the larger of the
+B and C full-vocabulary differences: the logit bar for a 36-layer run.
 
 Run from the repo root (about a minute on 8 cores):
     make -C oracle && python tests/golden/make_depth_noise.py
@@ -54,6 +57,18 @@ def attention_online(q, k, v, visible, scale=None):
     return (o / l).to(torch.bfloat16)
 
 
+def linear_splitk(x, w, chunk=512):
+    """R.linear's arithmetic (bf16 operands, fp32 products and sums, one bf16 rounding) with K
+    summed as fp32 partial dot products over `chunk`-wide K ranges, added in order -- the
+    split-K accumulation of the MFMA kernels, a valid reordering of the same sum."""
+    xf, wf = x.to(F32), w.to(F32)
+    acc = None
+    for k0 in range(0, x.shape[-1], chunk):
+        part = xf[..., k0:k0 + chunk] @ wf[:, k0:k0 + chunk].T
+        acc = part if acc is None else acc + part
+    return acc.to(torch.bfloat16)
+
+
 def main():
     torch.set_num_threads(os.cpu_count() or 8)
     depth = json.load(open(os.path.join(HERE, "depth.json")))
@@ -63,19 +78,24 @@ def main():
     ids = torch.cat([prompt, toks[:, :-1]], 1)                    # every position is a sample
     ref = R.Qwen3Ref.from_synth(1, 36)
     logits = {}
-    for name, fn in (("A", R.attention), ("B", attention_online)):
-        saved = R.attention
-        R.attention = fn
+    for name, att, lin in (("A", R.attention, R.linear), ("B", attention_online, R.linear),
+                           ("C", attention_online, linear_splitk)):
+        saved = R.attention, R.linear
+        R.attention, R.linear = att, lin
         try:
             logits[name] = ref.prefill(ids, ref.new_cache(1, ids.shape[1]), last_only=False)[0].float()
         finally:
-            R.attention = saved
-    la, lb = logits["A"], logits["B"]
+            R.attention, R.linear = saved
+    la, lb, lc = logits["A"], logits["B"], logits["C"]
+    absdiff_c = (la - lc).abs().amax(-1)
+    arg_c = lc.argmax(-1)
+    deficit_c = la.max(-1).values - la.gather(-1, arg_c[:, None])[:, 0]
     va, vb = la.topk(2, -1).values, lb.topk(2, -1).values
     gap_a, gap_b = va[:, 0] - va[:, 1], vb[:, 0] - vb[:, 1]
     arg_a, arg_b = la.argmax(-1), lb.argmax(-1)
     deficit = la.max(-1).values - la.gather(-1, arg_b[:, None])[:, 0]   # B's pick under A
     change = (gap_a - gap_b).abs()
+    absdiff = (la - lb).abs().amax(-1)                                # per position, full vocab
     diff = (arg_a != arg_b).nonzero()[:, 0].tolist()
     out = {"run": "config3: the 512 prompt ids + the stored oracle run's first 31 tokens "
                   "(depth.json), logits at every position",
@@ -86,6 +106,15 @@ def main():
            "gap_change_quantiles": {q: float(change.quantile(q)) for q in (0.5, 0.9, 0.99)},
            "argmax_differs": len(diff),
            "max_deficit_B_under_A": float(deficit.max()),
+           "max_abs_logit_diff": float(absdiff.max()),
+           "abs_logit_diff_quantiles": {q: float(absdiff.quantile(q)) for q in (0.5, 0.9, 0.99)},
+           "variant_C": "variant B with every projection summed as fp32 partials over 512-wide "
+                        "K ranges (split-K order), otherwise identical",
+           "argmax_differs_C": int((la.argmax(-1) != arg_c).sum()),
+           "max_deficit_C_under_A": float(deficit_c.max()),
+           "max_abs_logit_diff_C": float(absdiff_c.max()),
+           "abs_logit_diff_quantiles_C": {q: float(absdiff_c.quantile(q)) for q in (0.5, 0.9, 0.99)},
+           "logit_floor": float(max(absdiff.max(), absdiff_c.max())),
            "differing": [{"pos": i, "gap_A": float(gap_a[i]), "gap_B": float(gap_b[i]),
                           "deficit_B_under_A": float(deficit[i])} for i in diff]}
     with open(os.path.join(HERE, "depth_noise.json"), "w") as f:

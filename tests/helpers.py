@@ -86,12 +86,28 @@ def margin_report(tokens, ref_logits, margin=1e-2):
     return {"bad": bad, "steps": int(np.prod(tokens.shape)), "near": near, "used": used}
 
 
+def allowance_bound(steps):
+    """How many of `steps` judged steps may emit a near-tied id other than the reference
+    argmax at 36 layers: the larger rate at which a valid restatement of the oracle disagrees
+    with it on the argmax (depth_noise.json: 39 and 47 of 543 positions for variants B and C),
+    plus three Poisson standard deviations and one.  A regression that moves many near-tie
+    choices fails it even though each single choice stays within DEPTH_TIE."""
+    worst = max(DEPTH_NOISE["argmax_differs"], DEPTH_NOISE["argmax_differs_C"])
+    mean = steps * worst / DEPTH_NOISE["positions"]
+    return int(mean + 3.0 * mean ** 0.5 + 1.0)
+
+
 def margin_rule(tokens, ref_logits, margin=1e-2, what=""):
-    """margin_report's violations; prints how many steps the near-tie allowance covered."""
+    """margin_report's violations; prints how many steps the near-tie allowance covered.  With
+    margin >= DEPTH_TIE (a 36-layer run) the number of steps that used the allowance is held
+    to allowance_bound() as well (reported as one more violation)."""
     rep = margin_report(tokens, ref_logits, margin)
     print(f"[margin] {what} steps {rep['steps']} near-ties {rep['near']} "
           f"allowance used {rep['used']} violations {len(rep['bad'])}", flush=True)
-    return rep["bad"]
+    bad = list(rep["bad"])
+    if margin >= DEPTH_TIE - 1e-6 and rep["used"] > allowance_bound(rep["steps"]):
+        bad.append(("allowance used", rep["used"], allowance_bound(rep["steps"])))
+    return bad
 
 
 def fixture_rule(tokens, rec, tie=None):
@@ -116,3 +132,38 @@ def fixture_rule(tokens, rec, tie=None):
         return i + 1
     print(f"[fixture] all {len(ref)} steps identical", flush=True)
     return len(ref)
+
+
+def engine_step_logits(eng, prompt, N):
+    """Run the engine's own prefill and N - 1 decode steps (the graph replays generate()
+    performs) for a [B, S] prompt, and after every step recompute that step's logits from the
+    final residual it left: qd_lm_head_argmax over the step's x rows with the final RMSNorm,
+    fp32 logits before bf16 rounding.  Step 0's residual is the prefill's last prompt row per
+    sequence.  Returns (emitted ids [B, N], recomputed argmax ids [B, N], fp32 logits
+    [B, N, V]) on the host."""
+    from qdecode import _lib, ops
+    ids = torch.as_tensor(np.asarray(prompt), dtype=torch.int64)
+    B, S = ids.shape
+    sh = eng._state(B, S, N, 0)
+    m, st = eng.model, eng.stream
+    H, V = m.H, m.V
+    logits = torch.empty((N, B, V), dtype=torch.float32, device=m.device)
+    arg = torch.empty((N, B), dtype=torch.int64, device=m.device)
+    emitted = torch.empty((N, B), dtype=torch.int64, device=m.device)
+    ws = ops.workspace(_lib.LIB.qd_lm_head_workspace_bytes(B, V, H), m.device)
+    sh.start(ids, decode_next=N > 1)
+    T_last = S - (S - 1) // sh.chunk * sh.chunk              # rows of the last prefill chunk
+    with torch.cuda.stream(st):
+        last = sh.prefill.x[:B * T_last].view(B, T_last, H)[:, T_last - 1]
+        emitted[0].copy_(sh.kv.tok)
+        ops.lm_head_argmax(last, m.lm_head, m.final_norm, m.eps, tok=arg[0], logits=logits[0],
+                           ws=ws)
+        for t in range(1, N):
+            sh.decode.replay()
+            emitted[t].copy_(sh.kv.tok)
+            ops.lm_head_argmax(sh.decode.x, m.lm_head, m.final_norm, m.eps, tok=arg[t],
+                               logits=logits[t], ws=ws)
+    st.synchronize()
+    sh.decode.check()
+    return (emitted.T.cpu().numpy(), arg.T.cpu().numpy(),
+            logits.transpose(0, 1).contiguous().cpu())

@@ -84,6 +84,19 @@ def test_workspace_sizes(lib):
     assert L.qd_decode_step(C.byref(bad), C.byref(st), None) == lib.QD_EARG
 
 
+def test_noalloc_scratch_limits(lib):
+    """The documented limits of qd_decode_step_noalloc's static array at Qwen3-4B's shape:
+    batch 32 up to cap 106496 and batch 64 up to 40960 fit, one more key does not."""
+    L = lib.LIB
+    w = lib.Weights(36, 2560, 9728, 151936, 32, 8, 128, 1e-6, *([256] * 10))
+    lim = lib.QD_NOALLOC_SCRATCH_BYTES
+    assert lim == 16 << 20
+    for B, cap in ((32, 106496), (64, 40960)):
+        assert L.qd_decode_workspace_bytes(C.byref(w), B, cap) <= lim
+        assert L.qd_decode_workspace_bytes(C.byref(w), B, cap + 1) > lim
+    assert L.qd_decode_workspace_bytes(C.byref(w), 1, 1 << 20) <= lim       # B = 1: 8.6 MB
+
+
 def test_block_workspace_sizes(lib):
     """The block step's workspace at the benchmark shapes (no device here: 256 CUs assumed).
     Attention split partials exist only where the launch splits the keys and never grow with

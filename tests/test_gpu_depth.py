@@ -24,7 +24,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import DEPTH_TIE, GOLDEN, ensure_oracle_built, fixture_rule, margin_rule
+from helpers import (DEPTH_NOISE, DEPTH_TIE, GOLDEN, engine_step_logits, ensure_oracle_built,
+                     fixture_rule, margin_rule)
 from oracle import qwen3_ref as R
 from oracle import synth
 
@@ -68,6 +69,23 @@ def _teacher(ref, prompt_row, toks_row, what):
     return tl
 
 
+def _logit_gap(eng, prompt, toks, tl, what):
+    """The engine's per-step logits (recomputed from each step's final residual) against the
+    oracle's teacher-forced logits ``tl`` [B, N, V] (bf16) over the whole vocabulary.  Both on
+    the bf16 grid, the max-abs difference is held to the measured floor between equally valid
+    restatements of the oracle at this depth (tests/golden/depth_noise.json ``logit_floor``:
+    the online softmax, and the online softmax with split-K projection sums)."""
+    emitted, arg, lg = engine_step_logits(eng, prompt, toks.shape[1])
+    assert np.array_equal(emitted, toks) and np.array_equal(arg, toks), "replay differs"
+    d16 = (lg.to(torch.bfloat16).float() - tl.float()).abs().amax(-1)      # [B, N]
+    d32 = (lg - tl.float()).abs().amax(-1)
+    floor = DEPTH_NOISE["logit_floor"]
+    print(f"[logits] {what}: max-abs vs oracle per step (bf16) "
+          f"{[round(float(x), 4) for x in d16.flatten()]}; max bf16 {float(d16.max()):.4f}, "
+          f"fp32 {float(d32.max()):.4f}; floor between oracle variants {floor:.4f}", flush=True)
+    return float(d16.max()), floor
+
+
 def test_config3_end_to_end(eng36, ref36):
     prompt, c = _prompts("config3")
     say(f"config 3: 36 layers, B=1, S={c['S']}, N={c['N']}")
@@ -78,6 +96,8 @@ def test_config3_end_to_end(eng36, ref36):
     fixture_rule(toks[0], c["rows"][0], tie=DEPTH_TIE)
     tl = _teacher(ref36, prompt[0], toks[0], "config 3")
     assert margin_rule(toks, tl, margin=DEPTH_TIE, what="config 3, 36 layers") == []
+    worst, floor = _logit_gap(eng36, prompt, toks, tl, "config 3")
+    assert worst <= floor
 
 
 def test_config4_end_to_end(eng36, ref36):
@@ -90,6 +110,12 @@ def test_config4_end_to_end(eng36, ref36):
         fixture_rule(toks[rec["row"]], rec, tie=DEPTH_TIE)
     tl = _teacher(ref36, prompt[0], toks[0], "config 4 row 0")
     assert margin_rule(toks[:1], tl, margin=DEPTH_TIE, what="config 4 row 0") == []
+    emitted, arg, lg = engine_step_logits(eng36, prompt, c["N"])
+    assert np.array_equal(emitted, toks) and np.array_equal(arg, toks), "replay differs"
+    d16 = (lg[:1].to(torch.bfloat16).float() - tl.float()).abs().amax(-1)
+    print(f"[logits] config 4 row 0: max-abs vs oracle (bf16) {float(d16.max()):.4f}; floor "
+          f"{DEPTH_NOISE['logit_floor']:.4f}", flush=True)
+    assert float(d16.max()) <= DEPTH_NOISE["logit_floor"]
 
 
 def test_config5_tree_and_plain_at_8192(eng36):

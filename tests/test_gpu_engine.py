@@ -87,6 +87,48 @@ def test_config1_greedy(eng4, ref4):
     assert bad == []
 
 
+def test_config1_logits_against_transformers(eng4, ref4):
+    """Logits end to end at config 1: after every step the fp32 logits recomputed from the
+    step's final residual (qd_lm_head_argmax, final RMSNorm included) are compared with
+      * transformers' own logits (the golden run's top-8 values at the golden top-8 ids, bf16):
+        the engine's bf16-rounded logits within 2 bf16 ulp -- the bar the CPU oracle itself
+        meets against transformers (tests/test_oracle.py); the fp32 max-abs is reported;
+      * the CPU oracle's fp32 logits (same ids teacher-forced, final RMSNorm, fp32 product with
+        the tied embedding) over the whole vocabulary: max-abs reported per step;
+    and their argmax (bf16-rounded, lowest index) is the id the step emitted."""
+    say("config 1: per-step logits vs transformers' top-8 and the oracle's full vocabulary")
+    from helpers import engine_step_logits
+    emitted, arg, lg = engine_step_logits(eng4, CFG1["prompt"], 32)        # prompt: [1, 128]
+    assert np.array_equal(emitted, arg), (emitted, arg)
+    gold = np.array(CFG1["tokens"])
+    assert np.array_equal(emitted, gold), "the config-1 ids differ from the golden run"
+    ids = torch.tensor(CFG1["top_ids"])                                   # [32, 8]
+    want = torch.tensor(CFG1["top_values"], dtype=torch.float32)
+    got = lg[0].gather(-1, ids)
+    err = (got - want).abs()
+    ulps = (got.to(torch.bfloat16).float() - want).abs() / bf16_ulp(want)
+    print(f"vs transformers top-8: fp32 max-abs per step "
+          f"{[round(float(e), 4) for e in err.max(-1).values]}; overall {float(err.max()):.4f}; "
+          f"bf16-rounded max {float(ulps.max()):.1f} ulp", flush=True)
+    # the oracle's fp32 logits along the same ids
+    prompt = torch.tensor(CFG1["prompt"])
+    seq = torch.cat([prompt, torch.as_tensor(gold)[:, :-1]], 1)
+    S, cap = prompt.shape[1], seq.shape[1]
+    pos = torch.arange(cap)[None]
+    vis = torch.arange(cap)[None, None, :] <= pos[:, :, None]
+    with torch.inference_mode():
+        _, x = ref4.forward(seq, pos, pos, vis, ref4.new_cache(1, cap), return_hidden=True)
+        h = R.rmsnorm(x, ref4.p["model.norm.weight"], ref4.eps)[0, S - 1:]
+        ref32 = h.float() @ ref4.lm_head.float().T                        # [32, V]
+    d = (lg[0] - ref32).abs().amax(-1)
+    print(f"vs oracle fp32, whole vocabulary: max-abs per step "
+          f"{[round(float(e), 4) for e in d]}; overall {float(d.max()):.4f}", flush=True)
+    oracle_tf = (ref32.gather(-1, ids) - want).abs().max()
+    print(f"oracle fp32 vs transformers top-8 (the implementation floor): {float(oracle_tf):.4f}",
+          flush=True)
+    assert float(ulps.max()) <= 2.0
+
+
 def test_generate_resets_state_and_is_deterministic(eng4):
     say("generate x3 with an intervening prompt: identical ids")
     p1 = synth.prompt_ids(11, 1, 40).tolist()

@@ -245,8 +245,19 @@ def test_depth_noise_floor():
     vis = torch.ones(200, 200, dtype=torch.bool).tril()[None, None]
     a, b = R.attention(q, k, v, vis), mod.attention_online(q, k, v, vis)
     assert_ulp(a.float(), b.float(), 2, "online-softmax variant", abs_floor=2 ** -8 * v.abs().max().item())
+    # variant C's projections: the same product summed over 512-wide K ranges is a correct
+    # linear -- within 1 bf16 ulp of R.linear, and exactly R.linear for K <= 512
+    x = torch.randn(7, 2560, generator=g).to(torch.bfloat16)
+    w = (0.02 * torch.randn(300, 2560, generator=g)).to(torch.bfloat16)
+    assert_ulp(mod.linear_splitk(x, w).float(), R.linear(x, w).float(), 1, "split-K variant")
+    assert torch.equal(mod.linear_splitk(x[:, :512], w[:, :512]).float(),
+                       R.linear(x[:, :512].float(), w[:, :512].float()).to(torch.bfloat16).float())
     n = DEPTH_NOISE
     assert n["positions"] == 543 and 0 < n["argmax_differs"] < n["positions"] // 10
+    assert 0 < n["argmax_differs_C"] < n["positions"] // 10
     assert n["max_deficit_B_under_A"] > ORACLE_TIE
-    assert abs(DEPTH_TIE - n["max_deficit_B_under_A"]) < 1e-5
+    assert abs(DEPTH_TIE - max(n["max_deficit_B_under_A"], n["max_deficit_C_under_A"])) < 1e-5
     assert max(d["deficit_B_under_A"] for d in n["differing"]) == n["max_deficit_B_under_A"]
+    # the logit bar at depth: the larger full-vocabulary difference of the two variants, far
+    # above the north star's 2e-2 (which holds at 4 layers, tests/test_gpu_engine.py)
+    assert n["logit_floor"] == max(n["max_abs_logit_diff"], n["max_abs_logit_diff_C"]) > 2e-2

@@ -1,8 +1,14 @@
 """GPU: qd_decode_step_noalloc (the decode step for callers that cannot allocate, its split
 partials in the library's static device scratch) against qd_decode_step with a caller
 workspace, through the C ABI: bit-identical tokens, positions, residual stream and K/V caches
-after every step, for two calls in a row on different shapes (the second smaller, so it runs
-on scratch contents the first left behind), plus the size limit."""
+after every step.
+
+* The first test makes the process's first call of the entry point inside a hipGraph capture
+  (no other test file calls it), so the array's address is resolved during the capture; the
+  graph is then replayed with eager qd_decode_step work and synchronisation between replays.
+* Then calls in a row on shrinking shapes, each running on scratch contents the one before
+  left behind: B = 64 (tiled GEMMs, partials in the array), 8 and 3 (skinny GEMMs), 1 (GEMV).
+* The size limit is refused before any launch."""
 
 import ctypes as C
 
@@ -64,7 +70,45 @@ def _noalloc_state(_lib, kv, m):
     return st, bufs
 
 
-@pytest.mark.parametrize("B,S,steps", [(8, 300, 4), (3, 40, 3)], ids=["first-B8", "then-B3"])
+def _same(ra, kv_a, kv_b, bufs_b, step):
+    assert torch.equal(kv_a.tok, kv_b.tok), f"step {step}: tok {kv_a.tok} vs {kv_b.tok}"
+    assert torch.equal(kv_a.pos, kv_b.pos), f"step {step}: pos"
+    assert torch.equal(ra.x.view(torch.int16), bufs_b["x"].view(torch.int16)), f"step {step}: x"
+    assert torch.equal(kv_a.k.view(torch.int16), kv_b.k.view(torch.int16)), f"step {step}: K"
+    assert torch.equal(kv_a.v.view(torch.int16), kv_b.v.view(torch.int16)), f"step {step}: V"
+
+
+def test_noalloc_first_call_captured_in_graph(mods, model2):
+    _lib, M = mods
+    B, S, steps = 4, 96, 4
+    cap = S + steps + 1
+    say(f"qd_decode_step_noalloc captured into a hipGraph on its first call: B={B}, S={S}, "
+        f"{steps} replays against eager qd_decode_step")
+    stream, kv_a, kv_b = _prefilled_pair(M, _lib, model2, B, S, cap, seed=77)
+    ra = M.DecodeRunner(kv_a, stream, mega=False)
+    st_b, bufs_b = _noalloc_state(_lib, kv_b, model2)
+    torch.cuda.synchronize()
+    s = stream.cuda_stream
+    _lib.call("qd_graph_begin", s)
+    try:
+        rc = _lib.LIB.qd_decode_step_noalloc(C.byref(model2.qd), C.byref(st_b), s)
+    finally:
+        ex = C.c_void_p()
+        rc_end = _lib.LIB.qd_graph_end(s, C.byref(ex))
+    assert rc == 0 and rc_end == 0, (rc, rc_end)
+    try:
+        for step in range(steps):
+            with torch.cuda.stream(stream):
+                ra.enqueue()
+                _lib.call("qd_graph_launch", ex, s)
+            stream.synchronize()
+            _same(ra, kv_a, kv_b, bufs_b, step)
+    finally:
+        _lib.LIB.qd_graph_destroy(ex)
+
+
+@pytest.mark.parametrize("B,S,steps", [(64, 80, 3), (8, 300, 4), (3, 40, 3), (1, 50, 3)],
+                         ids=["first-B64", "then-B8", "then-B3", "then-B1"])
 def test_noalloc_step_matches_decode_step(mods, model2, B, S, steps):
     _lib, M = mods
     cap = S + steps + 1
@@ -81,11 +125,7 @@ def test_noalloc_step_matches_decode_step(mods, model2, B, S, steps):
             _lib.call("qd_decode_step_noalloc", C.byref(model2.qd), C.byref(st_b),
                       stream.cuda_stream)
         stream.synchronize()
-        assert torch.equal(kv_a.tok, kv_b.tok), f"step {step}: tok {kv_a.tok} vs {kv_b.tok}"
-        assert torch.equal(kv_a.pos, kv_b.pos), f"step {step}: pos"
-        assert torch.equal(ra.x.view(torch.int16), bufs_b["x"].view(torch.int16)), f"step {step}: x"
-        assert torch.equal(kv_a.k.view(torch.int16), kv_b.k.view(torch.int16)), f"step {step}: K"
-        assert torch.equal(kv_a.v.view(torch.int16), kv_b.v.view(torch.int16)), f"step {step}: V"
+        _same(ra, kv_a, kv_b, bufs_b, step)
 
 
 def test_noalloc_rejects_steps_beyond_its_scratch(mods, model2):
