@@ -1,9 +1,8 @@
-// The MFMA decode-attention workgroup (attn.hip's decode_attn_mfma_kernel, and the attention
-// phase of the persistent batched step in mega_batch.hip): see attn.hip for the design.
+// The MFMA decode-attention workgroup (attn.hip's decode_attn_mfma_kernel): see attn.hip for
+// the design.
 #pragma once
 
 #include "attn_core.h"
-#include "handoff.h"
 
 typedef short ba_v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) ba_v4i16_t ba_lds_v4i16_t;
@@ -28,25 +27,21 @@ struct DecodeMfmaLds {
   float wm[DM_NW][GRP], wl[DM_NW][GRP];
 };
 
-// Workgroup (split, kvh, b) of the launch below, nb sequences, with sm as its LDS.  HW (one key
-// split, part != nullptr): the qkv partials part[SQ][nb][W] are hand-off words (handoff.h), waited
-// for as they are loaded, and the output rows are stored as hand-off words; err is the error word
-// of the waits.  The arithmetic is the same.
-template <bool ROPE_ROW, bool HW = false, int SQ = 1>
+// Workgroup (split, kvh, b) of the launch below, nb sequences, with sm as its LDS.
+template <bool ROPE_ROW>
 __device__ __forceinline__ void decode_attn_mfma_block(
     DecodeMfmaLds& sm, int split, int kvh, int64_t b, int splits, int64_t nb,
     const bf16_t* __restrict__ qkv, int64_t qkv_stride, const bf16_t* __restrict__ qn,
     const bf16_t* __restrict__ kn, const bf16_t* __restrict__ cos_t,
     const bf16_t* __restrict__ sin_t, const int64_t* __restrict__ pos_ptr, bf16_t* k_cache,
     bf16_t* v_cache, int Hq, int Hkv, int64_t cap, int64_t chunk, float eps, float scale,
-    float* ws_acc, float* ws_ml, bf16_t* out, const float* __restrict__ part, int part_S,
-    uint32_t* err = nullptr) {
+    float* ws_acc, float* ws_ml, bf16_t* out, const float* __restrict__ part, int part_S) {
   typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
   typedef __attribute__((ext_vector_type(4))) float f32x4_t;
   // 16-byte units as a native vector: copies of HIP's uint4 struct are memcpys, which keep the
   // staging arrays out of registers
   typedef unsigned int u4v __attribute__((ext_vector_type(4)));
-  const int tid = HW ? hw_tid() : (int)threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = (int)threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int c = lane & 15, q4 = lane >> 4;
   const int64_t head_off = ((b * Hkv + kvh) * cap) * 128;
   const u4v* kb = reinterpret_cast<const u4v*>(k_cache + head_off);
@@ -70,49 +65,7 @@ __device__ __forceinline__ void decode_attn_mfma_block(
   const int64_t eq = (int64_t)(kvh * GRP + (wave & (GRP - 1))) * 128;
   const int64_t ek = (int64_t)(Hq + (wave == 1 ? Hkv : 0) + kvh) * 128;
   uint32_t q1, q2, k1, k2;
-  if constexpr (HW) {
-    // as below, from hand-off words: every split's four words are loaded before the first wait
-    const int64_t W = (int64_t)(Hq + 2 * Hkv) * 128;
-    const uint32_t* pw = reinterpret_cast<const uint32_t*>(part) + b * W;
-    const int64_t off[4] = {eq + lane, eq + lane + 64, ek + lane, ek + lane + 64};
-    uint32_t r[SQ][4];
-    auto fetch = [&]() {
-#pragma unroll
-      for (int sp = 0; sp < SQ; ++sp)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) r[sp][j] = hw_raw(pw + (int64_t)sp * nb * W + off[j]);
-    };
-    auto ready = [&]() {
-      bool ok = true;
-#pragma unroll
-      for (int sp = 0; sp < SQ; ++sp)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ok = ok && hw_ready(r[sp][j]);
-      return ok;
-    };
-    fetch();
-    if (!ready()) {                  // slow path: poll the unit's words (bounded)
-      for (uint32_t it = 1; !ready(); ++it) {
-        if ((it & 63) == 0) {
-          if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-          if (it >= HW_SPIN_LIMIT) {
-            __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-          }
-        }
-        __builtin_amdgcn_s_sleep(1);
-        fetch();
-      }
-    }
-    float a4[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) a4[j] = __uint_as_float(~r[0][j]);
-#pragma unroll
-    for (int sp = 1; sp < SQ; ++sp)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) a4[j] += __uint_as_float(~r[sp][j]);
-    q1 = f2bf(a4[0]); q2 = f2bf(a4[1]); k1 = f2bf(a4[2]); k2 = f2bf(a4[3]);
-  } else if (part) {
+  if (part) {
     // the qkv projection's split-K partials part[S][B][W]: each value is their sum in split
     // order rounded to bf16, the bits the projection's own epilogue stores when unsplit over
     // the same order
@@ -291,10 +244,7 @@ __device__ __forceinline__ void decode_attn_mfma_block(
     A1 += a * sm.u.wacc[w][h][d + 1];
   }
   const int64_t qrow = b * Hq + kvh * GRP + h;
-  if constexpr (HW) {
-    const float inv = 1.0f / L;
-    hw_put(reinterpret_cast<uint32_t*>(out) + (qrow * 128 + d) / 2, pack2(A0 * inv, A1 * inv));
-  } else if (splits == 1) {
+  if (splits == 1) {
     const float inv = 1.0f / L;
     *reinterpret_cast<uint32_t*>(out + qrow * 128 + d) = pack2(A0 * inv, A1 * inv);
   } else {

@@ -1,5 +1,5 @@
-// Cross-workgroup hand-off words of the persistent decode steps (mega.hip at B = 1,
-// mega_batch.hip at B >= 17): every produced value travels in 32-bit words (two bf16, or one
+// Cross-workgroup hand-off words of the persistent decode step (mega.hip, B = 1): every
+// produced value travels in 32-bit words (two bf16, or one
 // fp32 / index) written with agent-coherent stores and read with agent-coherent loads (the
 // cache policy of agent-scope relaxed atomics: single-copy atomic per word, coherent across the
 // XCDs' L2s).  A word holds its payload inverted (~payload), so 0 means "not written yet": a

@@ -544,66 +544,27 @@ static bool mega_ok(const qd_weights* w, int64_t batch) {
          mega_grid() > 0;
 }
 
-// the batched persistent step (17..32 sequences); cap <= 0: any cap this shape may take
-static bool mega_batch_shape_ok(const qd_weights* w, int64_t batch, int64_t cap) {
-  return w && batch > 1 && skinny_step_ok(w, batch) &&
-         mega_batch_ok(w->hidden, w->inter, w->n_q_heads, w->n_kv_heads, w->head_dim, batch, cap);
-}
-
 int qd_mega_supported(const qd_weights* w, int64_t batch) {
-  return weights_ok(w) && (mega_ok(w, batch) || mega_batch_shape_ok(w, batch, 0)) ? 1 : 0;
+  return weights_ok(w) && mega_ok(w, batch) ? 1 : 0;
 }
 
 int64_t qd_mega_workspace_bytes(const qd_weights* w, int64_t batch, int64_t cap) {
-  if (!weights_ok(w) || cap <= 0) return 0;
-  if (mega_ok(w, batch))
-    return mega_ctl_off(w, batch, cap) + 256 + mega_ll_bytes(w->n_layers, mega_splits(cap), mega_grid());
-  if (mega_batch_shape_ok(w, batch, cap))
-    return mega_ctl_off(w, batch, cap) + 256 + mega_batch_ll_bytes(w->n_layers, batch);
-  return 0;
+  if (!weights_ok(w) || cap <= 0 || !mega_ok(w, batch)) return 0;
+  return mega_ctl_off(w, batch, cap) + 256 + mega_ll_bytes(w->n_layers, mega_splits(cap), mega_grid());
 }
 
 int64_t qd_mega_ctl_offset(const qd_weights* w, int64_t batch, int64_t cap) {
-  if (!weights_ok(w) || cap <= 0 || (!mega_ok(w, batch) && !mega_batch_shape_ok(w, batch, cap)))
-    return -1;
+  if (!weights_ok(w) || cap <= 0 || !mega_ok(w, batch)) return -1;
   return mega_ctl_off(w, batch, cap);
 }
 
-// The batched persistent step: the embedding launch (+ the step's RoPE row), the persistent
-// kernel (layers and final RMSNorm) and the LM head, with qd_decode_step's workspace carving.
-static int mega_batch_step(const qd_weights* w, const qd_decode_state* st, hipStream_t s) {
-  const int64_t B = st->batch, cap = st->cap, H = w->hidden, V = w->vocab;
-  if (!skinny_step_ok(w, B, st)) return QD_EARG;
-  char* ws = static_cast<char*>(st->workspace);
-  const int64_t off = mega_ctl_off(w, B, cap);
-  Carver c(st->workspace);
-  (void)carve_decode_attn(c, B, w->n_q_heads, w->n_kv_heads, decode_attn_splits(B, w->n_kv_heads, cap));
-  LmWs lw = carve_lm(c, B, V, H);
-  (void)c.take<bf16_t>(B * H);
-  bf16_t* rope_row = c.take<bf16_t>(256);
-  launch_embed_rope(st->tok, w->embed, st->x, B, V, H, H, st->cos, st->sin, st->pos, cap, rope_row, s);
-  MegaBatchLaunch m;
-  m.w_qkv = w->w_qkv; m.w_o = w->w_o; m.w_gu = w->w_gu; m.w_down = w->w_down; m.ln1 = w->ln1;
-  m.ln2 = w->ln2; m.q_norm = w->q_norm; m.k_norm = w->k_norm; m.final_norm = w->final_norm;
-  m.rope = rope_row; m.k_cache = st->k_cache; m.v_cache = st->v_cache; m.pos = st->pos;
-  m.x = st->x; m.xn_out = lw.xn; m.ctl = reinterpret_cast<uint32_t*>(ws + off);
-  m.ll = reinterpret_cast<uint32_t*>(ws + off + 256); m.cap = cap; m.B = B; m.L = w->n_layers;
-  m.eps = w->eps;
-  const hipError_t e = launch_mega_batch(m, s);
-  if (e != hipSuccess) return (int)e;
-  return lm_head_normed(lw.xn, lm_weight(w), V, H, B, st->tok, st->pos, lw, s);
-}
-
 int qd_mega_step(const qd_weights* w, const qd_decode_state* st, void* stream) {
-  if (!weights_ok(w) || !st) return QD_EARG;
-  const bool batched = !mega_ok(w, st->batch);
-  if (batched && !mega_batch_shape_ok(w, st->batch, st->cap)) return QD_EARG;
+  if (!weights_ok(w) || !st || !mega_ok(w, st->batch)) return QD_EARG;
   if (st->cap <= 0 || !st->k_cache || !st->v_cache || !st->cos || !st->sin || !st->tok ||
       !st->pos || !st->x)
     return QD_EARG;
   const int64_t need = qd_mega_workspace_bytes(w, st->batch, st->cap);
   if (!st->workspace || need <= 0 || st->workspace_bytes < need) return QD_EWS;
-  if (batched) return mega_batch_step(w, st, S(stream));
   char* ws = static_cast<char*>(st->workspace);
   const int64_t off = mega_ctl_off(w, st->batch, st->cap);
   MegaLaunch m;

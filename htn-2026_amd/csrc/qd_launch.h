@@ -129,25 +129,6 @@ int64_t mega_ll_bytes(int L, int64_t splits, int grid);
 int64_t mega_splits(int64_t cap);
 hipError_t launch_mega_step(const MegaLaunch& m, hipStream_t s);
 int64_t decode_attn_chunk(int64_t cap, int64_t splits);
-// persistent batched decode step (mega_batch.hip): the layers and the final RMSNorm of the
-// skinny-GEMM step for 17..32 sequences
-struct MegaBatchLaunch {
-  const bf16_t *w_qkv, *w_o, *w_gu, *w_down, *ln1, *ln2, *q_norm, *k_norm, *final_norm;
-  const bf16_t* rope;   // the step's RoPE row (cos, sin), staged by launch_embed_rope
-  bf16_t *k_cache, *v_cache;
-  const int64_t* pos;
-  bf16_t* x;            // residual rows [B][H], the embedded tokens on entry
-  bf16_t* xn_out;       // final RMSNorm rows [B][H]
-  uint32_t* ctl;        // [0] epoch, [1] error; zero before the first launch
-  uint32_t* ll;         // mega_batch_ll_bytes, zero before the first launch with this B
-  int64_t cap, B;
-  int L;
-  float eps;
-};
-int mega_batch_grid();
-bool mega_batch_ok(int hidden, int inter, int hq, int hkv, int head_dim, int64_t B, int64_t cap);
-int64_t mega_batch_ll_bytes(int L, int64_t B);
-hipError_t launch_mega_batch(const MegaBatchLaunch& m, hipStream_t s);
 void launch_decode_attn(const bf16_t* qkv, int64_t qkv_stride, const bf16_t* qn, const bf16_t* kn,
                         const bf16_t* cos_t, const bf16_t* sin_t, const int64_t* pos,
                         bf16_t* k_cache, bf16_t* v_cache, int64_t B, int Hq, int Hkv, int64_t cap,

@@ -1,9 +1,8 @@
-// The skinny GEMM's workgroup body (gemm_skinny.hip's skinny_gemm_kernel, and the GEMM phases
-// of the persistent batched step in mega_batch.hip): see gemm_skinny.hip for the design.
+// The skinny GEMM's workgroup body (gemm_skinny.hip's skinny_gemm_kernel): see gemm_skinny.hip
+// for the design.
 #pragma once
 
 #include "qd_launch.h"
-#include "handoff.h"
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
@@ -42,10 +41,7 @@ struct SkinnyShape {
 };
 
 // One workgroup's block g (row block g / S, K range g % S) of the GEMM, with lds (LDS_U4 16-byte
-// units) as its staging and reduction space.  HW: the activation rows X are hand-off words
-// (handoff.h; the same element layout, each word holding two bf16 inverted), waited for as they
-// are staged, and the results (fp32 partials, or the bf16 outputs of the SwiGLU epilogue) are
-// stored as hand-off words; err is the error word of the waits.  The arithmetic is the same.
+// units) as its staging and reduction space.
 // register ring depth: chunks in flight per wave, within the register budget (no spills at 32
 // rows)
 template <int MT, int NT, int EPI>
@@ -54,17 +50,16 @@ constexpr int skinny_depth() {
   return L <= 8 ? QD_SK_DEPTH_SMALL : L <= 12 ? QD_SK_DEPTH_MID : QD_SK_DEPTH_LARGE;
 }
 
-template <int MT, int NT, int EPI, bool PART, int D, bool HW = false>
+template <int MT, int NT, int EPI, bool PART, int D>
 __device__ __forceinline__ void skinny_block(uint4* lds, const bf16_t* __restrict__ X, int64_t xs,
                                              int M, const bf16_t* __restrict__ W, int N, int K,
                                              int rows_per_wg, int S, int g, bf16_t* out,
                                              int64_t os, const bf16_t* res, int64_t rs,
-                                             float* part, uint32_t* err = nullptr) {
+                                             float* part) {
   using SH = SkinnyShape<MT, NT, EPI>;
   constexpr bool SW = SH::SW;
   constexpr int WT = SH::WT, WR = SH::WR, L = SH::L, LW = SH::LW;
-  static_assert(!HW || EPI == EPI_NONE || EPI == EPI_SWIGLU, "hand-off epilogues");
-  const int tid = HW ? hw_tid() : (int)threadIdx.x;
+  const int tid = (int)threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int rb = g / S, ks = g - rb * S;
@@ -107,8 +102,7 @@ __device__ __forceinline__ void skinny_block(uint4* lds, const bf16_t* __restric
     for (int i = 0; i < L; ++i) {
       const bool up = SW && i < LW && i >= LW / 2;
       const u32x4_t v = i < LW ? __builtin_amdgcn_raw_buffer_load_b128(up ? ru : rg, vofs[i], so, SK_NT)
-                               : __builtin_amdgcn_raw_buffer_load_b128(rx, vofs[i], so,
-                                                                       HW ? HW_CPOL : 0);
+                               : __builtin_amdgcn_raw_buffer_load_b128(rx, vofs[i], so, 0);
       buf[b][i] = make_uint4(v.x, v.y, v.z, v.w);
     }
   };
@@ -142,33 +136,6 @@ __device__ __forceinline__ void skinny_block(uint4* lds, const bf16_t* __restric
 #pragma unroll
     for (int b = 0; b < D; ++b) {
       if (cc + b < wc1) {
-        if constexpr (HW) {            // activation rows < M: wait for their words, then decode
-          const uint32_t so = (uint32_t)(cc + b) * (SK_KC * 2);
-          auto ready = [&]() {
-            bool ok = true;
-#pragma unroll
-            for (int i = LW; i < L; ++i) ok = ok && (8 * (i - LW) + lr >= M || hw_ready4(buf[b][i]));
-            return ok;
-          };
-          if (!ready()) {              // slow path: poll the chunk's words (bounded)
-            for (uint32_t it = 1; !ready(); ++it) {
-              if ((it & 63) == 0) {
-                if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-                if (it >= HW_SPIN_LIMIT) {
-                  __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                  break;
-                }
-              }
-              __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-              for (int i = LW; i < L; ++i) buf[b][i] = hw_load4(rx, vofs[i], so);
-            }
-          }
-#pragma unroll
-          for (int i = LW; i < L; ++i)
-            if (8 * (i - LW) + lr < M)
-              buf[b][i] = make_uint4(~buf[b][i].x, ~buf[b][i].y, ~buf[b][i].z, ~buf[b][i].w);
-        }
 #pragma unroll
         for (int i = 0; i < L; ++i) tile[sk_slot(8 * i + lr, lu)] = buf[b][i];
         load(b, cc + b + D);
@@ -195,13 +162,7 @@ __device__ __forceinline__ void skinny_block(uint4* lds, const bf16_t* __restric
     for (int w = 1; w < SK_WAVES; ++w) v += red[((w * WT + t) * MT + mt) * 64 + ln];
     const int64_t n = n0 + unit;
     if constexpr (PART) {
-      if constexpr (HW) {
-        hw_put4(reinterpret_cast<uint32_t*>(part + ((int64_t)ks * M + m) * N + n),
-                __float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
-                __float_as_uint(v[3]));
-      } else {
-        *reinterpret_cast<f32x4_t*>(part + ((int64_t)ks * M + m) * N + n) = v;
-      }
+      *reinterpret_cast<f32x4_t*>(part + ((int64_t)ks * M + m) * N + n) = v;
     } else {
       float y[4];
       if constexpr (SW) {
@@ -220,11 +181,7 @@ __device__ __forceinline__ void skinny_block(uint4* lds, const bf16_t* __restric
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[r] = v[r];
       }
-      if constexpr (HW) {
-        hw_put2(reinterpret_cast<uint32_t*>(out + m * os + n), pack2(y[0], y[1]), pack2(y[2], y[3]));
-      } else {
-        *reinterpret_cast<uint2*>(out + m * os + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
-      }
+      *reinterpret_cast<uint2*>(out + m * os + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
     }
   }
 }

@@ -8,8 +8,7 @@ The KV cache is [L, B, Hkv, cap, 128] bf16 per K and V (engine.py:178-181).
 
 ``DecodeRunner`` owns the per-step buffers of one batch size and replays the whole decode
 step as one hipGraph: at B = 1 on a device that supports it the persistent step (qd_mega_step,
-one launch; ``QD_MEGA=0`` selects the per-launch step; at 17..32 sequences qd_mega_step runs
-embed + one persistent launch + LM head, with ``QD_MEGA_BATCH=1``), otherwise qd_decode_step
+one launch; ``QD_MEGA=0`` selects the per-launch step), otherwise qd_decode_step
 (embed, 5-7 launches per layer, LM head + argmax + pos += 1);
 ``BlockRunner`` runs T tokens per sequence through every layer (tree verification, or a causal
 chunk of the prompt).  Every launch goes to the runner's own HIP stream (default priority).
@@ -179,15 +178,12 @@ class KVState:
 
 def mega_default(model, batch, cap=None):
     """Whether a decode step of `batch` sequences runs as the persistent kernel by default: at
-    B = 1 when the device and shape support it, unless QD_MEGA=0 is set.  The batched persistent
-    step (17..32 sequences with one attention key split at this cap) is bit-identical to the
-    per-launch step but not faster on MI355X (3.97 against 3.87 ms per B = 32 step: every
-    hand-off waits for the slowest of up to 256 producers plus a ~2-3 us memory round trip under
-    the weight stream, which costs what the launch boundaries did), so it runs only with
-    QD_MEGA_BATCH=1."""
-    if os.environ.get("QD_MEGA", "1") == "0":
-        return False
-    if batch > 1 and os.environ.get("QD_MEGA_BATCH", "0") != "1":
+    B = 1 when the device and shape support it, unless QD_MEGA=0 is set.  (A batched form for
+    17..32 sequences was bit-identical to the per-launch step and not faster on MI355X, 3.99
+    against 3.87 ms per B = 32 step: every hand-off waited for the slowest of up to 256
+    producers plus a memory round trip queued behind the weight stream, which cost what the
+    launch boundaries did; it was removed.)"""
+    if os.environ.get("QD_MEGA", "1") == "0" or batch != 1:
         return False
     if not _lib.LIB.qd_mega_supported(C.byref(model.qd), batch):
         return False
@@ -196,8 +192,7 @@ def mega_default(model, batch, cap=None):
 
 class DecodeRunner:
     """One greedy decode step for all B sequences, eager or as a hipGraph: the persistent
-    qd_mega_step (mega=True: B = 1, or 17..32 sequences) or qd_decode_step.  mega=None picks
-    mega_default()."""
+    qd_mega_step (mega=True, B = 1) or qd_decode_step.  mega=None picks mega_default()."""
 
     def __init__(self, kv, stream, mega=None):
         m = kv.model

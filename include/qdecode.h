@@ -210,14 +210,7 @@ int qd_decode_step_noalloc(const qd_weights *w, const qd_decode_state *st, void 
  * 1 = a hand-off wait expired (the step's results are invalid), 2 = pos outside [0, cap)
  * (nothing written).  The error word stays set until the caller clears it.
  * qd_mega_supported is 1 when this device and model shape can run it (batch 1, Qwen3-4B
- * layer shape, >= 256 CUs); otherwise the entry points return QD_EARG / 0 / -1.
- * At 17 <= batch <= 32 the same entry points run the batched persistent step: the embedding
- * launch, ONE persistent launch for the layers and the final RMSNorm (the skinny-GEMM step's
- * kernels, phase by phase, with the same arithmetic), then the LM head launches; bit-identical
- * to qd_decode_step at that batch (tokens, K/V, st->x), the same control words, and
- * qd_mega_workspace_bytes returns 0 (qd_mega_ctl_offset -1) for a cap whose attention needs
- * more than one key split (cap > 4096).  Like the batch-1 form it has no counterpart of its
- * own in the reference beyond the T6 tier cited above. */
+ * layer shape, >= 256 CUs); otherwise the entry points return QD_EARG / 0 / -1. */
 int qd_mega_supported(const qd_weights *w, int64_t batch);
 int64_t qd_mega_workspace_bytes(const qd_weights *w, int64_t batch, int64_t cap);
 int64_t qd_mega_ctl_offset(const qd_weights *w, int64_t batch, int64_t cap);

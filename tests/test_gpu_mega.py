@@ -1,9 +1,8 @@
 """GPU parity of the persistent decode step (qd_mega_step) with the per-launch step
 (qd_decode_step): bit-identical tokens, final residual, positions and K/V caches, step after
 step.  At B = 1 over attention split plans of 1 split, several splits (merge), and more units
-than workgroups; at 17 and 32 sequences (the batched persistent kernel) at short and ~2100-key
-contexts; plus hipGraph replays over 36 layers, the bad-position error path and the bounded
-waits (forced from the host through the error word)."""
+than workgroups; plus hipGraph replays over 36 layers, the bad-position error path and the
+bounded waits (forced from the host through the error word); other batch sizes are refused."""
 
 import ctypes as C
 
@@ -195,111 +194,15 @@ def test_engine_mega_matches_per_launch(mods, monkeypatch):
     assert t1 == t2
 
 
-# ------------------------------------------------------------------ batched persistent step
-@pytest.fixture(scope="module")
-def model4b(mods):
+def test_persistent_step_is_batch_one_only(mods, model4):
+    """The persistent entry points serve B = 1 only: other batch sizes are refused (the
+    per-launch step serves them), and the host never picks them."""
     _lib, M = mods
-    m = M.Qwen3Model.synthetic(n_layers=4, seed=0)
-    if not _lib.LIB.qd_mega_supported(C.byref(m.qd), 32):
-        pytest.skip("batched persistent step unsupported on this device")
-    return m
-
-
-@pytest.mark.parametrize("B,S,N", [(32, 40, 12), (17, 40, 8), (32, 2100, 6)],
-                         ids=["b32-short", "b17-short", "b32-2100-keys"])
-def test_mega_batch_matches_decode_step(mods, model4b, B, S, N):
-    _lib, M = mods
-    cap = M.kv_capacity(S, N)
-    say(f"batched mega vs per-launch step: 4 layers, B={B}, S={S}, N={N}, cap={cap}")
-    stream, kv_a, kv_b = _prefilled_pair(M, _lib, model4b, S, cap, seed=S + B, B=B)
-    ra = M.DecodeRunner(kv_a, stream, mega=False)
-    rb = M.DecodeRunner(kv_b, stream, mega=True)
-    assert rb.mega
-    torch.cuda.synchronize()
-    for step in range(N - 1):
-        with torch.cuda.stream(stream):
-            ra.enqueue()
-            rb.enqueue()
-        stream.synchronize()
-        _assert_same(ra, rb, kv_a, kv_b, step)
-    epoch, err = rb.mega_status()
-    assert err == 0 and epoch == N - 1
-
-
-def test_mega_batch_default_and_cap_limit(mods, model4b, monkeypatch):
-    """The batched persistent step runs only when asked for (QD_MEGA_BATCH=1), and then only where
-    one attention key split covers the cap."""
-    _lib, M = mods
-    say("batched mega default: off; with QD_MEGA_BATCH=1 on at cap 2200, off at cap 5000")
-    monkeypatch.delenv("QD_MEGA_BATCH", raising=False)
-    assert not M.mega_default(model4b, 32, 2200)
-    monkeypatch.setenv("QD_MEGA_BATCH", "1")
-    assert M.mega_default(model4b, 32, 2200)
-    assert not M.mega_default(model4b, 32, 5000)
-    assert not M.mega_default(model4b, 16, 2200)
-
-
-def test_mega_batch_graph_replay_36_layers(mods):
-    _lib, M = mods
-    say("batched mega graph replays vs per-launch step: 36 layers, B=32, S=256, 8 steps")
-    model = M.Qwen3Model.synthetic(n_layers=36, seed=1)
-    if not _lib.LIB.qd_mega_supported(C.byref(model.qd), 32):
-        pytest.skip("batched persistent step unsupported on this device")
-    B, S, N = 32, 256, 9
-    stream, kv_a, kv_b = _prefilled_pair(M, _lib, model, S, M.kv_capacity(S, N), seed=9, B=B)
-    ra = M.DecodeRunner(kv_a, stream, mega=False)
-    rb = M.DecodeRunner(kv_b, stream, mega=True)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        ra.capture()
-        rb.capture()
-    for step in range(N - 1):
-        with torch.cuda.stream(stream):
-            ra.replay()
-            rb.replay()
-        stream.synchronize()
-        _assert_same(ra, rb, kv_a, kv_b, step)
-        torch.zeros(1 << 20, device=model.device).add_(1.0)
-        torch.cuda.synchronize()
-    epoch, err = rb.mega_status()
-    assert err == 0 and epoch == N - 1
-    ra.close()
-    rb.close()
-
-
-def test_mega_batch_bad_position_sets_error(mods, model4b):
-    """pos == cap: the persistent kernel writes nothing and reports error 2 (the LM head after it
-    still runs, as in the per-launch step, and its token is not to be used)."""
-    _lib, M = mods
-    say("batched mega with pos == cap: error word 2, K/V untouched")
-    B, S, N = 32, 40, 8
-    stream, _, kv = _prefilled_pair(M, _lib, model4b, S, M.kv_capacity(S, N), seed=5, B=B)
-    r = M.DecodeRunner(kv, stream, mega=True)
-    kv.pos.fill_(kv.cap)
-    k0, v0 = kv.k.clone(), kv.v.clone()
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        r.enqueue()
-    epoch, err = r.mega_status()
-    assert err == 2 and epoch == 0
-    assert torch.equal(kv.k, k0) and torch.equal(kv.v, v0)
-    with pytest.raises(RuntimeError):
-        r.check()
-
-
-def test_mega_batch_waits_are_bounded(mods, model4b):
-    """A preset error word makes every wait of the batched kernel give up after a bounded number
-    of polls: the step completes and reports the error."""
-    _lib, M = mods
-    say("batched mega with the error word preset: completes, error stays set")
-    B, S, N = 32, 40, 8
-    stream, _, kv = _prefilled_pair(M, _lib, model4b, S, M.kv_capacity(S, N), seed=6, B=B)
-    r = M.DecodeRunner(kv, stream, mega=True)
-    r.err_word.fill_(1)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        r.enqueue()
-    epoch, err = r.mega_status()
-    assert err == 1 and epoch == 1
-    assert ((kv.tok >= 0) & (kv.tok < model4b.V)).all()
-
+    say("qd_mega_supported / workspace / ctl offset refuse B != 1")
+    for B in (2, 17, 32):
+        assert _lib.LIB.qd_mega_supported(C.byref(model4.qd), B) == 0
+        assert _lib.LIB.qd_mega_workspace_bytes(C.byref(model4.qd), B, 2200) == 0
+        assert _lib.LIB.qd_mega_ctl_offset(C.byref(model4.qd), B, 2200) == -1
+        assert not M.mega_default(model4, B, 2200)
+    assert _lib.LIB.qd_mega_supported(C.byref(model4.qd), 1) == 1
+    assert M.mega_default(model4, 1, 2200)
