@@ -1,7 +1,7 @@
 """Decode benchmark on one MI355X: Qwen3-4B-shaped bf16 greedy decode through the HIP engine.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-b32] [--no-tree] [--no-cpu]
-                    [--no-layer]
+                    [--no-layer] [--no-api]
 
 Workloads (the benchmark's configurations 2-5; configuration 1 is the CPU parity case):
   value  config 3 -- 36 layers, B=1, prompt 512, up to 256 new tokens: decode tok/s over K timed
@@ -10,7 +10,10 @@ Workloads (the benchmark's configurations 2-5; configuration 1 is the CPU parity
   b32    config 4 -- 36 layers, B=32, prompts of 2048, up to 128 new tokens (same method).
   tree   config 5 -- tree verification, B=4, context 8192, 64-node random trees: the verify
          forward timed with HIP events (bytes/s and MFMA TFLOP/s), plus an end-to-end
-         generate_tree (tokens per pass, wall-clock tok/s).
+         generate_tree of 256 tokens (tokens per pass, host ms per pass, wall-clock tok/s) and,
+         beside it, plain B=4 decode of the same prompt and length through generate().
+  api    configs 3 and 4 through Engine.generate, measured the reference's way: batch x output
+         tokens / total generate wall time, prefill included (first call and warm call).
   layer_kernels  config 2 -- embedding gather, residual-add + RMSNorm, QK-norm + RoPE (+ K/V
          write), SwiGLU at B in {1, 8, 64}: us per launch (1000 launches in one hipGraph) and
          algorithmic GB/s.
@@ -20,6 +23,8 @@ Workloads (the benchmark's configurations 2-5; configuration 1 is the CPU parity
   step_ms  per-step spread (median, p90, min, max) of the same K steps replayed again with an
          event after each step (the headline timing has no events between steps).
 Weights are seeded random-init N(0, 0.02) generated on the device; prompt ids uniform.
+
+cpu_baseline_configs: config 1 in full and config 4's decode step (capped) on the CPU oracle.
 
 Roofline: at B=1 the step is ONE kernel (mega_step_kernel, the persistent decode step), so
 the dominant kernel is the step itself: achieved = algorithmic bytes per step (weights + the
@@ -122,7 +127,34 @@ def decode_run(eng, B, S, N, warmup, steps, seed):
                 "achieved_gbs": step_bytes / (ms * 1e-3) / 1e9}
 
 
-def tree_run(eng, B=4, S=8192, T=64, K=20, warmup=3, N_e2e=64, seed=5):
+def api_run(eng, B, S, N, seed, what):
+    """The reference's own measure (QWEN_ENGINE_CONTRACT.md:93,102): batch x output tokens /
+    total Engine.generate time, prefill included, through the drop-in API as a user gets it
+    (tree speculation gate on its default, ``ENGINE_TREE=auto``).  The first call on a shape
+    also captures the decode graph and runs the tree gate where it applies; it is reported
+    apart, and the second call (same shape, a different prompt) is the measured one."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    out = {"workload": what, "B": B, "prompt_len": S, "new_tokens": N}
+    for key in ("first_call", "warm"):
+        prompt = rng.integers(0, eng.model.V, size=(B, S)).tolist()
+        t0 = time.perf_counter()
+        n = 0
+        first_tok = None
+        for step in eng.generate(prompt, N):
+            n += 1
+            if first_tok is None:
+                first_tok = time.perf_counter() - t0
+        wall = time.perf_counter() - t0
+        assert n == N
+        out[key] = {"wall_s": round(wall, 4), "tok_s": round(B * N / wall, 1),
+                    "first_token_s": round(first_tok, 4)}
+    out["tree_gate"] = eng.tree_log.get((B, S, N))
+    out["value"], out["unit"] = out["warm"]["tok_s"], "tok/s"
+    return out
+
+
+def tree_run(eng, B=4, S=8192, T=64, K=20, warmup=3, N_e2e=256, seed=5):
     """Config 5: tree verification.  Prefill B prompts of S tokens, draft one random T-node tree
     per sequence (qdecode.tree.random_tree_drafter, branching 4-4-2-2), then time K replays of
     the verify forward (qd_block_step over B*T rows: every weight once + every row's K/V) with
@@ -173,13 +205,26 @@ def tree_run(eng, B=4, S=8192, T=64, K=20, warmup=3, N_e2e=64, seed=5):
     dense = 36 * (6144 * 2560 + 2560 * 4096 + 19456 * 2560 + 2560 * 9728) + m.V * m.H
     gemm_flop = 2.0 * B * T * dense
     attn_flop = 4.0 * B * T * 32 * 128 * ctx * m.L
-    # end to end (same shape, host loop included)
+    # end to end (same shape, host loop included): tree verification of N_e2e tokens, then
+    # plain B=4 decode of the same prompt and N_e2e (the comparison that matters when random
+    # drafts accept ~1 token per pass)
     prompt = ids.tolist()
     w0 = time.perf_counter()
     out = list(eng.generate_tree(prompt, N_e2e, tr.random_tree_drafter(seed + 1), T=T))
     wall = time.perf_counter() - w0
     stats = eng.tree_stats
     acc = stats["accepted"]
+    host_ms = stats["host_ms"]
+    mode = eng.tree_mode
+    try:
+        eng.tree_mode = "0"
+        eng.shape = None
+        list(eng.generate(prompt, N_e2e))                 # shape + graph capture, untimed
+        p0 = time.perf_counter()
+        plain = list(eng.generate(prompt, N_e2e))
+        plain_wall = time.perf_counter() - p0
+    finally:
+        eng.tree_mode = mode
     return {"workload": f"config 5: tree verification, B={B}, context {S}, {T}-node random "
                         f"4-4-2-2 trees", "verify_ms": round(ms, 4), "verify_steps": K,
             "bytes_per_verify": int(nbytes), "achieved_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
@@ -190,7 +235,11 @@ def tree_run(eng, B=4, S=8192, T=64, K=20, warmup=3, N_e2e=64, seed=5):
             "prefill_s": round(prefill_s, 3),
             "e2e": {"new_tokens": N_e2e, "passes": stats["passes"],
                     "tokens_per_pass": round(sum(acc) / max(len(acc), 1), 3),
-                    "wall_s": round(wall, 3), "tok_s": round(B * len(out) / wall, 1)}}
+                    "host_ms_per_pass": round(sum(host_ms) / max(len(host_ms), 1), 4),
+                    "wall_s": round(wall, 3), "tok_s": round(B * len(out) / wall, 1)},
+            "plain_e2e": {"new_tokens": N_e2e, "wall_s": round(plain_wall, 3),
+                          "tok_s": round(B * len(plain) / plain_wall, 1),
+                          "note": "generate() with trees off, same prompt, prefill included"}}
 
 
 def time_gu_kernel(eng, sh, reps=20):
@@ -227,25 +276,26 @@ def time_gu_kernel(eng, sh, reps=20):
     return us, nbytes
 
 
-def time_read_ceiling(eng, reps=20, grids=(768, 2048, 4864)):
-    """The read rate one launch can reach over the gate/up GEMV's weight bytes: qd_read_probe
-    (non-temporal 16-byte loads, nothing computed or written) over the same 36 layers'
-    W_gate|W_up, captured as one hipGraph of 36 launches like time_gu_kernel and replayed; the
-    best of three grids.  Returns (us per launch, grid, bytes per launch)."""
+def time_read_ceiling(eng, reps=20, grids=(768, 2048, 4864), bufs=None):
+    """The read rate one launch can reach over the gate/up GEMV's weight bytes (or over each of
+    `bufs`, equal-sized contiguous tensors): qd_read_probe (non-temporal 16-byte loads, nothing
+    computed or written) over the same 36 layers' W_gate|W_up, captured as one hipGraph of 36
+    launches like time_gu_kernel and replayed; the best of the grids.  Returns (us per launch,
+    grid, bytes per launch)."""
     import ctypes as C
 
     import torch
     from qdecode import _lib
     m, st = eng.model, eng.stream
     sink = torch.zeros(1, dtype=torch.int32, device=m.device)
-    nbytes = m.w_gu[0].numel() * m.w_gu[0].element_size()
+    bufs = [m.w_gu[l] for l in range(m.L)] if bufs is None else bufs
+    nbytes = bufs[0].numel() * bufs[0].element_size()
     best = None
     for g in grids:
         with torch.cuda.stream(st):
             _lib.call("qd_graph_begin", st.cuda_stream)
             try:
-                for l in range(m.L):
-                    w = m.w_gu[l]
+                for w in bufs:
                     assert w.is_contiguous() and w.numel() * w.element_size() == nbytes
                     _lib.call("qd_read_probe", w.data_ptr(), nbytes, g, sink.data_ptr(),
                               st.cuda_stream)
@@ -265,10 +315,31 @@ def time_read_ceiling(eng, reps=20, grids=(768, 2048, 4864)):
             e1.record(st)
         torch.cuda.synchronize()
         _lib.LIB.qd_graph_destroy(ex)
-        us = e0.elapsed_time(e1) * 1e3 / (reps * m.L)
+        us = e0.elapsed_time(e1) * 1e3 / (reps * len(bufs))
         if best is None or us < best[0]:
             best = (us, g)
     return best[0], best[1], nbytes
+
+
+def read_floors(eng, kv_bytes):
+    """The streaming floor of one launch of each B=32 decode-step size: qd_read_probe over each
+    projection's 36 per-layer weight tensors, and over four buffers of one layer's K/V bytes,
+    best of grids 256-4096 (what a launch of that many bytes can read at all, ramp-up and drain
+    included)."""
+    import torch
+    m = eng.model
+    grids = (256, 512, 1024, 2048, 4096)
+    out = {}
+    for name, t in (("qkv", m.w_qkv), ("o", m.w_o), ("gate_up", m.w_gu), ("down", m.w_down)):
+        us, g, nb = time_read_ceiling(eng, reps=10, grids=grids, bufs=[t[l] for l in range(m.L)])
+        out[name] = {"bytes": nb, "us": round(us, 3), "grid": g,
+                     "tb_s": round(nb / (us * 1e-6) / 1e12, 3)}
+    kv = torch.empty((4, int(kv_bytes) // 2), dtype=torch.bfloat16, device=m.device)
+    us, g, nb = time_read_ceiling(eng, reps=10, grids=grids, bufs=[kv[i] for i in range(4)])
+    out["kv_layer"] = {"bytes": nb, "us": round(us, 3), "grid": g,
+                       "tb_s": round(nb / (us * 1e-6) / 1e12, 3)}
+    del kv
+    return out
 
 
 def layer_kernels(reps=1000):
@@ -379,11 +450,12 @@ def _graph_time_us(fn, reps, rounds=5):
     return e0.elapsed_time(e1) * 1e3 / (rounds * reps)
 
 
-def layer_kernels_large(reps=20):
+def layer_kernels_large(reps=20, scale=1):
     """The config-2 layer kernels at row counts where bandwidth binds (>= 100 MB per launch;
     the config's own B <= 64 moves 10 KB - 3.7 MB): embedding gather of 16384 ids, add +
     RMSNorm of 8192 rows, QK-norm + RoPE + K/V write of 8192 token rows (one sequence at
-    positions 0..8191, i.e. the whole config-2 position range), SwiGLU of 4096 rows.  Bytes
+    positions 0..8191, i.e. the whole config-2 position range), SwiGLU of 4096 rows; with
+    scale=4, four times those rows (the prefill chunk's 32768 rows for the norms).  Bytes
     are algorithmic (every input read once, every output written once).  `copy_gbs` is a
     device-to-device copy of the same number of bytes (half read, half written) by the
     runtime, the read+write stream these kernels compare to; `frac` is of 8 TB/s."""
@@ -407,13 +479,13 @@ def layer_kernels_large(reps=20):
                     "copy_gbs": round(nbytes / (cus * 1e-6) / 1e9, 1)})
 
     table = torch.randn((V, H), generator=g, device=dev).to(bf)
-    n = 16384
+    n = 16384 * scale
     ids = torch.randint(0, V, (n,), generator=g, device=dev)
     emb = torch.empty((n, H), dtype=bf, device=dev)
     record("embed_gather", n, 2 * n * H * 2, lambda: ops.embed_gather(ids, table, out=emb))
     del table, emb
 
-    n = 8192
+    n = 8192 * scale
     x = torch.randn((n, H), generator=g, device=dev).to(bf)
     r = torch.randn((n, H), generator=g, device=dev).to(bf)
     w = torch.ones(H, dtype=bf, device=dev)
@@ -422,7 +494,7 @@ def layer_kernels_large(reps=20):
            lambda: ops.add_rmsnorm(r, w, 1e-6, x=x, res_out=ro, y=y))
     del x, r, ro, y
 
-    T = 8192
+    T = 8192 * scale
     qkv = torch.randn((T, (Hq + 2 * Hkv) * 128), generator=g, device=dev).to(bf)
     cos = torch.randn((T, 128), generator=g, device=dev).to(bf)
     sin = torch.randn((T, 128), generator=g, device=dev).to(bf)
@@ -436,7 +508,7 @@ def layer_kernels_large(reps=20):
                                     1, T, Hq, Hkv, 1e-6))
     del qkv, q_out, kc, vc
 
-    n = 4096
+    n = 4096 * scale
     gu = torch.randn((n, 2 * I), generator=g, device=dev).to(bf)
     act = torch.empty((n, I), dtype=bf, device=dev)
     record("swiglu", n, 3 * n * I * 2, lambda: ops.swiglu(gu, out=act))
@@ -465,13 +537,14 @@ def cpu_baseline(budget_s=15.0, prompt_len=512):
     ref = qwen3_ref.Qwen3Ref.from_synth(1, 36)
     gen_s = time.perf_counter() - t0
     prompt = torch.as_tensor(synth.prompt_ids(1, 1, prompt_len))
-    cap = prompt_len + 64
+    max_steps = 400
+    cap = prompt_len + max_steps + 1
     cache = ref.new_cache(1, cap)
     with torch.inference_mode():
         lg = ref.prefill(prompt, cache)
         tok = qwen3_ref.argmax_lowest(lg[:, -1])
         n, t1 = 0, time.perf_counter()
-        while n < 3 or (time.perf_counter() - t1 < budget_s and n < 400):
+        while n < 3 or (time.perf_counter() - t1 < budget_s and n < max_steps):
             lg = ref.decode(tok, prompt_len + n, cache)
             tok = qwen3_ref.argmax_lowest(lg)
             n += 1
@@ -491,6 +564,52 @@ def cpu_baseline(budget_s=15.0, prompt_len=512):
                        f"mask) of {cpu}")}
 
 
+def cpu_config1():
+    """Config 1 in full on the CPU oracle: 4 layers (seed 0), B=1, 128-token prompt, 32 greedy
+    tokens, prefill included (the reference's CPU path, engine.py:963-972)."""
+    import torch
+    sys.path.insert(0, ROOT)
+    from oracle import qwen3_ref, synth
+    ref = qwen3_ref.Qwen3Ref.from_synth(0, 4)
+    prompt = torch.as_tensor(synth.prompt_ids(0, 1, 128))
+    with torch.inference_mode():
+        t0 = time.perf_counter()
+        toks, _ = ref.greedy(prompt, 32)
+        dt = time.perf_counter() - t0
+    return {"workload": "config 1: 4 layers, B=1, S=128, N=32, greedy with prefill (full run)",
+            "value": round(32 / dt, 3), "unit": "tok/s", "wall_s": round(dt, 3),
+            "cores": torch.get_num_threads(), "kind": "port"}
+
+
+def cpu_config4(budget_s=12.0, B=32, ctx=2048):
+    """Config 4's decode step on the CPU oracle, capped: B=32 sequences at context 2048, 36
+    layers.  The 32 x 2048-token prefill (minutes on the host) is replaced by a KV cache
+    filled with seeded bf16 values (the step's cost does not depend on them), then greedy
+    decode steps are timed for ~budget_s."""
+    import torch
+    sys.path.insert(0, ROOT)
+    from oracle import qwen3_ref
+    ref = qwen3_ref.Qwen3Ref.from_synth(1, 36)
+    g = torch.Generator().manual_seed(4)
+    cap = ctx + 64
+    kc, vc = ref.new_cache(B, cap)
+    kc[:, :, :, :ctx].copy_(torch.randn(kc[:, :, :, :ctx].shape, generator=g).to(kc.dtype))
+    vc[:, :, :, :ctx].copy_(torch.randn(vc[:, :, :, :ctx].shape, generator=g).to(vc.dtype))
+    tok = torch.randint(0, ref.embed.shape[0], (B,), generator=g)
+    n = 0
+    with torch.inference_mode():
+        t0 = time.perf_counter()
+        while n < 2 or (time.perf_counter() - t0 < budget_s and n < 200):
+            tok = qwen3_ref.argmax_lowest(ref.decode(tok, ctx + n, (kc, vc)))
+            n += 1
+        dt = time.perf_counter() - t0
+    return {"workload": f"config 4 decode step, capped: 36 layers, B={B}, context {ctx} "
+                        f"(KV cache filled with seeded values instead of the 32 x 2048 prefill), "
+                        f"{n} steps ({dt:.1f} s)",
+            "value": round(B * n / dt, 3), "unit": "tok/s", "ms_per_step": round(dt * 1e3 / n, 2),
+            "cores": torch.get_num_threads(), "kind": "port"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -501,6 +620,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-tree", action="store_true")
     ap.add_argument("--no-layer", action="store_true", help="skip the config-2 kernel microbench")
+    ap.add_argument("--no-api", action="store_true", help="skip the Engine.generate runs")
+    ap.add_argument("--tree-steps", type=int, default=20, help="timed verify forwards")
+    ap.add_argument("--tree-e2e", type=int, default=256, help="tokens of the end-to-end tree run")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB: the reference "
@@ -572,27 +694,52 @@ def main():
                                  "frac": round(r32["achieved_gbs"] / PEAK_HBM_GBS, 4),
                                  "bytes_per_step": int(r32["bytes_per_step"])},
                "prefill_s": round(r32["prefill_s"], 3)}
+        # one layer's K/V read at the timed steps' mean context
+        kv_layer = r32["B"] * (2048 + 10 + (r32["K"] - 1) / 2 + 1) * eng.model.kv_bytes_per_token / eng.model.L
         eng.shape = None
         del sh32
+        torch.cuda.empty_cache()
+        b32["read_floors"] = read_floors(eng, kv_layer // 16 * 16)
+        log("B=32 read floors: " + ", ".join(f"{k} {v['us']} us" for k, v in b32["read_floors"].items()))
+        torch.cuda.empty_cache()
+
+    api = None
+    if not a.no_api:
+        eng.shape = None
+        torch.cuda.empty_cache()
+        api = {"config3": api_run(eng, 1, 512, 256, 13, "config 3 through Engine.generate: "
+                                  "B=1, prompt 512, 256 new tokens")}
+        log(f"API config 3: {api['config3']['warm']['tok_s']} tok/s (prefill included), first "
+            f"call {api['config3']['first_call']['tok_s']}")
+        if not a.no_b32:
+            eng.shape = None
+            torch.cuda.empty_cache()
+            api["config4"] = api_run(eng, 32, 2048, 128, 14, "config 4 through Engine.generate: "
+                                     "B=32, prompts 2048, 128 new tokens")
+            log(f"API config 4: {api['config4']['warm']['tok_s']} tok/s (prefill included)")
+        eng.shape = None
         torch.cuda.empty_cache()
 
     tree = None
     if not a.no_tree:
         eng.shape = None
         torch.cuda.empty_cache()
-        tree = tree_run(eng)
+        tree = tree_run(eng, K=a.tree_steps, N_e2e=a.tree_e2e)
         log(f"tree verify (B=4, ctx 8192, T=64): {tree['verify_ms']:.3f} ms, "
             f"{tree['achieved_gbs']:.0f} GB/s, {tree['achieved_tflops']:.1f} TFLOP/s; "
             f"e2e {tree['e2e']['tok_s']} tok/s, prefill {tree['prefill_s']:.2f}s")
         eng.shape = None
         torch.cuda.empty_cache()
 
-    cpu = None
+    cpu = cpu_more = None
     if not a.no_cpu:
         eng = None
         torch.cuda.empty_cache()
         cpu = cpu_baseline(a.cpu_budget)
         log(f"cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} threads")
+        cpu_more = {"config1": cpu_config1(), "config4": cpu_config4()}
+        log(f"cpu config 1: {cpu_more['config1']['value']} tok/s; config 4 capped: "
+            f"{cpu_more['config4']['value']} tok/s")
 
     gu_gbs = gu_bytes / (us * 1e-6) / 1e9
     gemv = {"bound": "hbm", "kernel": "gemv_kernel gate/up + SwiGLU (B=1, per-launch step)",
@@ -636,7 +783,9 @@ def main():
         "tree": tree,
         "layer_kernels": layer,
         "layer_kernels_large": layer_large,
+        "api": api,
         "cpu_baseline": cpu,
+        "cpu_baseline_configs": cpu_more,
     }
     print(json.dumps(line), flush=True)
 

@@ -9,15 +9,23 @@ configs 3-5 name) for:
 
   config3  B=1, 512 prompt ids, 32 greedy tokens
   config4  rows 0 and 31 of B=32 x 2048 prompt ids, 4 greedy tokens (rows are independent)
-  config5  rows 0 and 1 of B=4 x 8192 prompt ids, 8 greedy tokens
+  config5  all 4 rows of B=4 x 8192 prompt ids, 32 greedy tokens
 
 and stores, per row, the prompt's generator seed, the greedy ids, and per step the top-2
 logits (bf16 values as floats) and their ids.  Prompts are ``synth.prompt_ids(seed, B, S)``.
 The prompt is prefilled in causal chunks of 1024 tokens (the same function; it bounds the
 fp32 score matrices), then decoded one token at a time with the KV cache (engine.py:963-972).
 
-Run from the repo root (about 10 minutes on 8 cores):
-    make -C oracle && python tests/golden/make_depth_golden.py
+Teacher forcing of recorded engine runs ("teacher"): the engine's ids at configs 4 and 5
+(engine_runs.json, recorded on MI355X by record_engine_runs.py) are fed to the oracle from the
+same prefilled cache, and per step the oracle's top-2 gap, the emitted id's deficit under the
+oracle's maximum and the top-2 ids and values are stored (plain runs also store the oracle's
+logits at its top-16 ids and at 48 ids drawn per step, for the GPU test's logit check).  A
+row's runs share one prefill: its cache is copied after the prompt.
+
+Run from the repo root (config3 + config4 + config5 + teacher forcing: about 40 minutes on 8
+cores; `--only config5` recomputes one config and keeps the others):
+    make -C oracle && python tests/golden/make_depth_golden.py [--only NAME ...]
 """
 
 import json
@@ -34,21 +42,24 @@ from oracle import qwen3_ref as R  # noqa: E402
 from oracle import synth  # noqa: E402
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "depth.json")
+RUNS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "engine_runs.json")
 CHUNK = 1024
+SAMPLE_TOP, SAMPLE_RAND = 16, 48
 
 # name -> (prompt seed, B, S, N, rows kept)
 CONFIGS = {
     "config3": (301, 1, 512, 32, [0]),
     "config4": (401, 32, 2048, 4, [0, 31]),
-    "config5": (501, 4, 8192, 8, [0, 1]),
+    "config5": (501, 4, 8192, 32, [0, 1, 2, 3]),
 }
+# rows of the recorded engine runs that are teacher-forced
+TEACHER_ROWS = {"config4": [0, 5, 10, 15, 20, 25, 30, 31], "config5": [0, 1, 2, 3]}
 
 
-def greedy_row(ref, prompt, n_new):
-    """Greedy decode of one prompt row: (ids, per-step top-2 values and ids)."""
+def prefill_row(ref, prompt, cap):
+    """The prompt through the oracle in causal chunks: (cache, bf16 logits [V] after it)."""
     S = prompt.shape[0]
-    cache = ref.new_cache(1, S + n_new)
-    cap = S + n_new
+    cache = ref.new_cache(1, cap)
     j = torch.arange(cap)
     for c0 in range(0, S, CHUNK):
         ids = prompt[None, c0:c0 + CHUNK]
@@ -56,34 +67,95 @@ def greedy_row(ref, prompt, n_new):
         pos = c0 + torch.arange(T)[None, :]
         vis = j[None, None, :] <= pos[:, :, None]
         logits = ref.forward(ids, pos, pos, vis, cache, last_only=True)[:, -1]
+    return cache, logits[0]
+
+
+def greedy_from(ref, cache, S, logits, n_new):
+    """Greedy decode from a prefilled cache: (ids, per-step top-2 values and ids)."""
     toks, top_v, top_i = [], [], []
     for t in range(n_new):
         if t:
-            logits = ref.decode(torch.tensor([toks[-1]]), S + t - 1, cache)
-        v, i = logits.float().topk(2, dim=-1)
-        top_v.append(v[0].tolist())
-        top_i.append(i[0].tolist())
-        toks.append(int(R.argmax_lowest(logits)[0]))
+            logits = ref.decode(torch.tensor([toks[-1]]), S + t - 1, cache)[0]
+        v, i = logits.float().topk(2)
+        top_v.append(v.tolist())
+        top_i.append(i.tolist())
+        toks.append(int(R.argmax_lowest(logits[None])[0]))
     return toks, top_v, top_i
 
 
+def teacher_from(ref, cache, S, logits, feed, sample_seed=None):
+    """The oracle along the given ids (teacher forcing): per step the top-2 gap, the fed id's
+    deficit under the maximum, the top-2 ids / values and, with sample_seed, the logits at
+    the top-16 ids and at 48 ids drawn per step."""
+    steps = []
+    for t, tok in enumerate(feed):
+        if t:
+            logits = ref.decode(torch.tensor([feed[t - 1]]), S + t - 1, cache)[0]
+        lf = logits.float()
+        v, i = lf.topk(2)
+        rec = {"gap": float(v[0] - v[1]), "deficit": float(v[0] - lf[tok]),
+               "top2_ids": i.tolist(), "top2_values": v.tolist()}
+        if sample_seed is not None:
+            g = torch.Generator().manual_seed(sample_seed * 1000 + t)
+            ids = torch.cat([lf.topk(SAMPLE_TOP).indices,
+                             torch.randint(0, lf.shape[0], (SAMPLE_RAND,), generator=g)])
+            rec["sample_ids"] = ids.tolist()
+            rec["sample_values"] = lf[ids].tolist()
+        steps.append(rec)
+    return steps
+
+
+def clone(cache):
+    return tuple(c.clone() for c in cache)
+
+
 def main():
+    import argparse
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--only", nargs="*", default=None, help="configs to recompute")
+    a = ap.parse_args()
     torch.set_num_threads(os.cpu_count() or 8)
     t0 = time.time()
     ref = R.Qwen3Ref.from_synth(1, 36)
     print(f"weights ready in {time.time() - t0:.1f} s", flush=True)
-    out = {"weights": "synth seed 1, 36 layers, std 0.02, norm weights 1, tied",
-           "prompt": "synth.prompt_ids(seed, B, S)[row]", "chunk": CHUNK}
+    out = json.load(open(OUT)) if a.only and os.path.exists(OUT) else {}
+    out.update({"weights": "synth seed 1, 36 layers, std 0.02, norm weights 1, tied",
+                "prompt": "synth.prompt_ids(seed, B, S)[row]", "chunk": CHUNK})
+    runs = json.load(open(RUNS)) if os.path.exists(RUNS) else {}
+    teacher = out.get("teacher", {}) if a.only else {}
     for name, (seed, B, S, N, rows) in CONFIGS.items():
+        if a.only and name not in a.only:
+            continue
         prompts = torch.as_tensor(synth.prompt_ids(seed, B, S))
-        recs = []
-        for r in rows:
+        run = runs.get(name)
+        kinds = [k for k in ("plain", "tree") if run and k in run]
+        n_feed = run["N"] if run else 0
+        recs, trecs = [], []
+        for r in sorted(set(rows) | set(TEACHER_ROWS.get(name, []) if run else [])):
             t1 = time.time()
-            toks, tv, ti = greedy_row(ref, prompts[r], N)
-            recs.append({"row": r, "tokens": toks, "top2_values": tv, "top2_ids": ti,
-                         "margins": [a - b for a, b in tv]})
-            print(f"{name} row {r}: {toks} ({time.time() - t1:.1f} s)", flush=True)
+            cache, logits = prefill_row(ref, prompts[r], S + max(N, n_feed))
+            if r in rows:
+                toks, tv, ti = greedy_from(ref, clone(cache), S, logits, N)
+                recs.append({"row": r, "tokens": toks, "top2_values": tv, "top2_ids": ti,
+                             "margins": [x - y for x, y in tv]})
+                print(f"{name} row {r}: {toks} ({time.time() - t1:.1f} s)", flush=True)
+            if run and r in TEACHER_ROWS.get(name, []):
+                tr = {"row": r}
+                for k in kinds:
+                    feed = run[k][r]
+                    tr[k] = {"tokens": feed,
+                             "steps": teacher_from(ref, clone(cache), S, logits, feed,
+                                                   sample_seed=r if k == "plain" else None)}
+                    worst = max(st["deficit"] for st in tr[k]["steps"])
+                    print(f"{name} row {r} engine {k}: teacher-forced, worst deficit {worst:.4f}",
+                          flush=True)
+                trecs.append(tr)
+            del cache
         out[name] = {"seed": seed, "B": B, "S": S, "N": N, "rows": recs}
+        if run:
+            teacher[name] = {"seed": seed, "B": B, "S": S, "N": n_feed, "rows": trecs,
+                             "engine_runs_library_sha256": runs.get("library_sha256")}
+        out["teacher"] = teacher
         with open(OUT, "w") as f:
             json.dump(out, f, indent=1)
     print(f"wrote {OUT} in {time.time() - t0:.1f} s", flush=True)

@@ -86,6 +86,36 @@ def test_add_rmsnorm(ops, B):
     assert_ulp(y2.cpu(), R.rmsnorm(r, w), 2, "rmsnorm")
 
 
+def test_add_rmsnorm_many_rows(ops):
+    """Launches of more rows than 32 workgroups per CU take the multi-row kernel (each
+    workgroup walks rows with the next row's loads in flight); its per-row arithmetic is the
+    one-workgroup-per-row kernel's, so the bits are the same: 32 x CUs + 100 rows at once
+    against the same rows in pieces of at most 2048 (the per-row kernel), with and without the
+    residual input, also in place (res_out = residual), and within 2 ulp of the oracle."""
+    n = 32 * torch.cuda.get_device_properties(0).multi_processor_count + 100
+    say(f"add_rmsnorm {n} rows: multi-row kernel == per-row kernel, bitwise")
+    g = torch.Generator().manual_seed(123)
+    x, r = rnd(g, n, 2560).to(DEV), rnd(g, n, 2560, scale=4.0).to(DEV)
+    w = (rnd(g, 2560, scale=0.1) + 1).to(DEV)
+    r_all, y_all = ops.add_rmsnorm(r, w, 1e-6, x=x)
+    y0_all = ops.rmsnorm(r, w, 1e-6)
+    r_pc, y_pc, y0_pc = torch.empty_like(r), torch.empty_like(r), torch.empty_like(r)
+    for a in range(0, n, 2048):
+        b = min(n, a + 2048)
+        ops.add_rmsnorm(r[a:b], w, 1e-6, x=x[a:b], res_out=r_pc[a:b], y=y_pc[a:b])
+        ops.rmsnorm(r[a:b], w, 1e-6, y=y0_pc[a:b])
+    rr = r.clone()                                       # in place: res_out = residual
+    _, y_in = ops.add_rmsnorm(rr, w, 1e-6, x=x, res_out=rr)
+    sync()
+    assert torch.equal(r_all, r_pc) and torch.equal(rr, r_pc)
+    assert torch.equal(y_all.view(torch.int16), y_pc.view(torch.int16))
+    assert torch.equal(y_in.view(torch.int16), y_pc.view(torch.int16))
+    assert torch.equal(y0_all.view(torch.int16), y0_pc.view(torch.int16))
+    r_ref, y_ref = R.add_rmsnorm(x[:512].cpu(), r[:512].cpu(), w.cpu())
+    assert torch.equal(r_all[:512].cpu(), r_ref)
+    assert_ulp(y_all[:512].cpu(), y_ref, 2, "add_rmsnorm, many rows")
+
+
 @pytest.mark.parametrize("B", [1, 8, 64])
 def test_qk_norm_rope_kv_write(ops, B):
     say(f"qk_norm_rope B={B} positions U[0,8192)")
