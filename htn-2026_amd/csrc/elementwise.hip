@@ -217,10 +217,80 @@ __global__ __launch_bounds__(256) void part_add_rmsnorm_kernel(
   }
 }
 
+// 256 < hidden / 8 <= 512 (hidden 2560: 320 chunks): chunks tid and tid + 256 of the row, with
+// every load of both -- all splits' partials, the residual, the norm weights -- issued before
+// the first add (the second chunk's address clamped to the first's where it lies past the row,
+// its results dropped); the arithmetic and its order are part_add_rmsnorm_kernel's, so the bits
+// are the same.  The guarded per-chunk loop above issues the second chunk's loads only after the
+// first chunk's sums: two memory round trips instead of one.
+template <int SC>
+__global__ __launch_bounds__(256) void part_add_rmsnorm2_kernel(
+    const float* __restrict__ part, int64_t rows, bf16_t* res, const bf16_t* __restrict__ w,
+    bf16_t* __restrict__ y, int64_t hidden, float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int nch = (int)(hidden / 8);
+  uint4* rr = reinterpret_cast<uint4*>(res + row * hidden);
+  const uint4* wr = reinterpret_cast<const uint4*>(w);
+  uint4* yr = reinterpret_cast<uint4*>(y + row * hidden);
+  const int c0 = threadIdx.x, c1 = threadIdx.x + 256;
+  const bool has1 = c1 < nch;
+  const int cc[2] = {c0, has1 ? c1 : c0};
+  float4 pv[2][SC][2];
+  uint4 rv[2], gv[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+#pragma unroll
+    for (int sp = 0; sp < SC; ++sp) {
+      const float4* ps = reinterpret_cast<const float4*>(part + ((int64_t)sp * rows + row) * hidden) + 2 * cc[q];
+      pv[q][sp][0] = ps[0];
+      pv[q][sp][1] = ps[1];
+    }
+    rv[q] = rr[cc[q]];
+    gv[q] = wr[cc[q]];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    if (q == 1 && !has1) break;
+    float4 a = pv[q][0][0], b = pv[q][0][1];
+#pragma unroll
+    for (int sp = 1; sp < SC; ++sp) {
+      const float4 a2 = pv[q][sp][0], b2 = pv[q][sp][1];
+      a.x += a2.x; a.y += a2.y; a.z += a2.z; a.w += a2.w;
+      b.x += b2.x; b.y += b2.y; b.z += b2.z; b.w += b2.w;
+    }
+    const uint4 r = rv[q];
+    uint4 o;
+    o.x = pack2(bflo(r.x) + rbf(a.x), bfhi(r.x) + rbf(a.y));
+    o.y = pack2(bflo(r.y) + rbf(a.z), bfhi(r.y) + rbf(a.w));
+    o.z = pack2(bflo(r.z) + rbf(b.x), bfhi(r.z) + rbf(b.y));
+    o.w = pack2(bflo(r.w) + rbf(b.z), bfhi(r.w) + rbf(b.w));
+    rv[q] = o;
+    ss += sumsq8(o);
+  }
+  const float rstd = rstd_of(block_sum256(ss, red), (int)hidden, eps);
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    if (q == 1 && !has1) break;
+    yr[cc[q]] = norm8(rv[q], gv[q], rstd);
+    rr[cc[q]] = rv[q];                           // each thread writes back the chunks it read
+  }
+}
+
 void launch_part_add_rmsnorm(const float* part, int S, int64_t rows, bf16_t* res, const bf16_t* w,
                              bf16_t* y, int64_t hidden, float eps, hipStream_t s) {
   if (rows <= 0) return;
   const dim3 g((unsigned)rows), b(256);
+  if (hidden / 8 > 256 && hidden / 8 <= 512) {
+    switch (S) {
+      case 1: part_add_rmsnorm2_kernel<1><<<g, b, 0, s>>>(part, rows, res, w, y, hidden, eps); return;
+      case 2: part_add_rmsnorm2_kernel<2><<<g, b, 0, s>>>(part, rows, res, w, y, hidden, eps); return;
+      case 4: part_add_rmsnorm2_kernel<4><<<g, b, 0, s>>>(part, rows, res, w, y, hidden, eps); return;
+      case 6: part_add_rmsnorm2_kernel<6><<<g, b, 0, s>>>(part, rows, res, w, y, hidden, eps); return;
+      default: break;
+    }
+  }
   switch (S) {
     case 1: part_add_rmsnorm_kernel<1><<<g, b, 0, s>>>(part, S, rows, res, w, y, hidden, eps); break;
     case 2: part_add_rmsnorm_kernel<2><<<g, b, 0, s>>>(part, S, rows, res, w, y, hidden, eps); break;
@@ -329,6 +399,54 @@ static int64_t arn_cus() {
   return cus;
 }
 
+// add_rmsnorm_kernel for 256 < hidden / 8 <= 512 with both chunks' loads issued first (as
+// part_add_rmsnorm2_kernel; same arithmetic, same bits).
+template <bool HAS_X>
+__global__ __launch_bounds__(256) void add_rmsnorm2_kernel(
+    const bf16_t* __restrict__ x, const bf16_t* res, const bf16_t* __restrict__ w,
+    bf16_t* res_out, bf16_t* __restrict__ y, int64_t hidden, int64_t in_stride,
+    int64_t y_stride, float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int nch = (int)(hidden / 8);
+  const uint4* rr = reinterpret_cast<const uint4*>(res + row * in_stride);
+  const uint4* wr = reinterpret_cast<const uint4*>(w);
+  uint4* yr = reinterpret_cast<uint4*>(y + row * y_stride);
+  const int c0 = threadIdx.x, c1 = threadIdx.x + 256;
+  const bool has1 = c1 < nch;
+  const int cc[2] = {c0, has1 ? c1 : c0};
+  uint4 rv[2], xv[2], gv[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    rv[q] = rr[cc[q]];
+    if (HAS_X) xv[q] = reinterpret_cast<const uint4*>(x + row * in_stride)[cc[q]];
+    gv[q] = wr[cc[q]];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    if (q == 1 && !has1) break;
+    if (HAS_X) {
+      uint4 r = rv[q];
+      const uint4 a = xv[q];
+      r.x = pack2(bflo(a.x) + bflo(r.x), bfhi(a.x) + bfhi(r.x));
+      r.y = pack2(bflo(a.y) + bflo(r.y), bfhi(a.y) + bfhi(r.y));
+      r.z = pack2(bflo(a.z) + bflo(r.z), bfhi(a.z) + bfhi(r.z));
+      r.w = pack2(bflo(a.w) + bflo(r.w), bfhi(a.w) + bfhi(r.w));
+      rv[q] = r;
+    }
+    ss += sumsq8(rv[q]);
+  }
+  const float rstd = rstd_of(block_sum256(ss, red), (int)hidden, eps);
+  uint4* ro = res_out ? reinterpret_cast<uint4*>(res_out + row * in_stride) : nullptr;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    if (q == 1 && !has1) break;
+    yr[cc[q]] = norm8(rv[q], gv[q], rstd);
+    if (HAS_X && ro) ro[cc[q]] = rv[q];
+  }
+}
+
 void launch_add_rmsnorm(const bf16_t* x, const bf16_t* res, const bf16_t* w, bf16_t* res_out,
                         bf16_t* y, int64_t rows, int64_t hidden, int64_t in_stride,
                         int64_t y_stride, float eps, hipStream_t s) {
@@ -341,6 +459,15 @@ void launch_add_rmsnorm(const bf16_t* x, const bf16_t* res, const bf16_t* w, bf1
     else
       add_rmsnorm_rows_kernel<false><<<dim3((unsigned)grid), dim3(256), 0, s>>>(
           x, res, w, res_out, y, rows, hidden, in_stride, y_stride, eps);
+    return;
+  }
+  if (hidden / 8 > 256 && hidden / 8 <= 512) {
+    if (x)
+      add_rmsnorm2_kernel<true><<<dim3((unsigned)rows), dim3(256), 0, s>>>(
+          x, res, w, res_out, y, hidden, in_stride, y_stride, eps);
+    else
+      add_rmsnorm2_kernel<false><<<dim3((unsigned)rows), dim3(256), 0, s>>>(
+          x, res, w, res_out, y, hidden, in_stride, y_stride, eps);
     return;
   }
   add_rmsnorm_kernel<<<dim3((unsigned)rows), dim3(256), 0, s>>>(x, res, w, res_out, y, hidden,
@@ -399,8 +526,24 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   // grid (token blocks of QKR_ROWS, sequence b, head group of 16): no integer division
   const int grp = threadIdx.x >> 3, j = threadIdx.x & 7;
   const int head = (int)blockIdx.z * 16 + (grp & 15);
-  if (head >= Hq + 2 * Hkv) return;            // whole 8-lane groups leave together
   const int64_t b = blockIdx.y;
+  // The workgroup's QKR_ROWS RoPE rows, unpacked to fp32 once and shared by its 16 heads
+  // through LDS: thread t stages 16-byte unit (t & 15) of the cos (t & 16 == 0) or sin row of
+  // token row t >> 5 (clamped into the table; rows outside it are skipped below).  The unpack
+  // is exact, so the arithmetic is the same as unpacking per head.
+  __shared__ float4 rope_lds[QKR_ROWS][2][32];
+  {
+    const int r = (int)threadIdx.x >> 5, unit = threadIdx.x & 15, tab = (threadIdx.x >> 4) & 1;
+    const int64_t tr = (int64_t)blockIdx.x * QKR_ROWS + r;
+    const int64_t p0s = mode == POS_T ? 0 : mode == POS_SHARED ? pos[0] : pos[b];
+    int64_t rp = mode == POS_TREE ? p0s + depth[b * T + (tr < T ? tr : T - 1)] : p0s + tr;
+    rp = rp < 0 ? 0 : (rp >= table_len ? table_len - 1 : rp);
+    const uint4 v = reinterpret_cast<const uint4*>((tab ? sin_t : cos_t) + rp * 128)[unit];
+    rope_lds[r][tab][2 * unit] = make_float4(bflo(v.x), bfhi(v.x), bflo(v.y), bfhi(v.y));
+    rope_lds[r][tab][2 * unit + 1] = make_float4(bflo(v.z), bfhi(v.z), bflo(v.w), bfhi(v.w));
+  }
+  __syncthreads();
+  if (head >= Hq + 2 * Hkv) return;            // whole 8-lane groups leave together
   // the run's first row: uniform over the wave (waves 0-1 the first run, 2-3 the second), so
   // every row-dependent value below lives in scalar registers
   const int run = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 7);
@@ -484,17 +627,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     }
     return;
   }
-  // RoPE rows (clamped for the load; rows outside the table are skipped below): row i + 1's
-  // loads are issued when row i starts, so at most two rows of cos / sin are live
-  auto rope_row = [&](int i, uint4 (&cs)[4]) {
-    const int64_t r = rpos[i] < 0 ? 0 : (rpos[i] >= table_len ? table_len - 1 : rpos[i]);
-    const uint4* cr = reinterpret_cast<const uint4*>(cos_t + r * 128);
-    const uint4* sr = reinterpret_cast<const uint4*>(sin_t + r * 128);
-    cs[0] = cr[j]; cs[1] = cr[j + 8];
-    cs[2] = sr[j]; cs[3] = sr[j + 8];
-  };
-  uint4 csr[2][4];
-  rope_row(0, csr[0]);
   float wl[8], wh[8];
   {
     const uint4* wsrc = reinterpret_cast<const uint4*>(head < Hq ? qn : kn);
@@ -532,8 +664,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   for (int i = 0; i < QKR_RPG; ++i) {
     const int64_t t = t0 + i;
     if (t >= T) break;                         // uniform over the wave
-    if (i + 1 < QKR_RPG) rope_row(i + 1, csr[(i + 1) & 1]);
-    __builtin_amdgcn_sched_barrier(0);         // keep the next row's loads here, not hoisted
     if (rpos[i] < 0 || rpos[i] >= table_len) continue;
     const int64_t row = b * T + t;
     // one packed word (dims 2k, 2k + 1 of the lane's lo and hi runs) at a time, each closed by a
@@ -541,10 +671,15 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     // the waves a SIMD can hold
     const uint32_t* X1 = reinterpret_cast<const uint32_t*>(&xl[i]);
     const uint32_t* X2 = reinterpret_cast<const uint32_t*>(&xh[i]);
-    const uint32_t* C1 = reinterpret_cast<const uint32_t*>(&csr[i & 1][0]);
-    const uint32_t* C2 = reinterpret_cast<const uint32_t*>(&csr[i & 1][1]);
-    const uint32_t* S1 = reinterpret_cast<const uint32_t*>(&csr[i & 1][2]);
-    const uint32_t* S2 = reinterpret_cast<const uint32_t*>(&csr[i & 1][3]);
+    // cos / sin of dims 8j .. 8j + 7 (c1, s1) and 64 + 8j .. (c2, s2) of this row, fp32
+    const float4* rl = rope_lds[run * QKR_RPG + i][0];
+    const float4* sl = rope_lds[run * QKR_RPG + i][1];
+    const float4 c1v[2] = {rl[2 * j], rl[2 * j + 1]}, c2v[2] = {rl[16 + 2 * j], rl[17 + 2 * j]};
+    const float4 s1v[2] = {sl[2 * j], sl[2 * j + 1]}, s2v[2] = {sl[16 + 2 * j], sl[17 + 2 * j]};
+    const float* c1 = reinterpret_cast<const float*>(c1v);
+    const float* c2 = reinterpret_cast<const float*>(c2v);
+    const float* s1 = reinterpret_cast<const float*>(s1v);
+    const float* s2 = reinterpret_cast<const float*>(s2v);
     uint32_t ow[8];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -556,10 +691,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
       y2a *= wh[2 * k]; y2b *= wh[2 * k + 1];
       rbf2(y1a, y1b); rbf2(y2a, y2b);
       // rotation: o1 = bf16(y1 c1) + bf16(-y2 s1), o2 = bf16(y2 c2) + bf16(y1 s2)
-      float p1a = y1a * bflo(C1[k]), p1b = y1b * bfhi(C1[k]);
-      float q1a = -y2a * bflo(S1[k]), q1b = -y2b * bfhi(S1[k]);
-      float p2a = y2a * bflo(C2[k]), p2b = y2b * bfhi(C2[k]);
-      float q2a = y1a * bflo(S2[k]), q2b = y1b * bfhi(S2[k]);
+      float p1a = y1a * c1[2 * k], p1b = y1b * c1[2 * k + 1];
+      float q1a = -y2a * s1[2 * k], q1b = -y2b * s1[2 * k + 1];
+      float p2a = y2a * c2[2 * k], p2b = y2b * c2[2 * k + 1];
+      float q2a = y1a * s2[2 * k], q2b = y1b * s2[2 * k + 1];
       rbf2(p1a, p1b); rbf2(q1a, q1b); rbf2(p2a, p2b); rbf2(q2a, q2b);
       ow[k] = pack2(p1a + q1a, p1b + q1b);
       ow[4 + k] = pack2(p2a + q2a, p2b + q2b);
