@@ -760,7 +760,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const bf16_t* __restrict__ 
   const uint4 g = reinterpret_cast<const uint4*>(gu + row * gu_stride)[c];
   const uint4 u = reinterpret_cast<const uint4*>(gu + row * gu_stride + inter)[c];
   uint4 o;
-#define SW(lo, hi, G, U) pack2(rbf(silu_f(lo(G))) * lo(U), rbf(silu_f(hi(G))) * hi(U))
+#define SW(lo, hi, G, U) pack2(silu_rbf(lo(G)) * lo(U), silu_rbf(hi(G)) * hi(U))
   o.x = SW(bflo, bfhi, g.x, u.x);
   o.y = SW(bflo, bfhi, g.y, u.y);
   o.z = SW(bflo, bfhi, g.z, u.z);

@@ -72,7 +72,7 @@ __device__ __forceinline__ void gemm_epilogue(EpiLds<MT, EPI, NW>& sm, const f32
       float u = red2[0][e];
 #pragma unroll
       for (int w2 = 1; w2 < NW; ++w2) u += red2[w2][e];
-      y = rbf(silu_f(rbf(v))) * rbf(u);
+      y = silu_rbf(rbf(v)) * rbf(u);
     } else {
       y = v;
     }
@@ -431,7 +431,7 @@ __global__ __launch_bounds__(512) void gemm_stream_kernel(
               if constexpr (EPI == EPI_RES) {
                 y = bf2f(res[m * res_stride + n]) + rbf(v);
               } else if constexpr (SW) {
-                y = rbf(silu_f(rbf(v))) * rbf(acc2[i][r]);
+                y = silu_rbf(rbf(v)) * rbf(acc2[i][r]);
               } else {
                 y = v;
               }

@@ -286,7 +286,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(
           float y[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            y[r] = rbf(silu_f(rbf(acc[nt][mt][r]))) * rbf(acc[nt + 2][mt][r]);
+            y[r] = silu_rbf(rbf(acc[nt][mt][r])) * rbf(acc[nt + 2][mt][r]);
           *reinterpret_cast<uint2*>(out + m * out_stride + n) =
               make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
         }
@@ -444,7 +444,7 @@ __global__ __launch_bounds__(512, 2) void gemm_tile8_kernel(
       const int64_t n = (int64_t)nb * 64 + 16 * wn + 4 * q;
       float y[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) y[r] = rbf(silu_f(rbf(acc[0][mt][r]))) * rbf(acc[1][mt][r]);
+      for (int r = 0; r < 4; ++r) y[r] = silu_rbf(rbf(acc[0][mt][r])) * rbf(acc[1][mt][r]);
       *reinterpret_cast<uint2*>(out + m * out_stride + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
     } else {
 #pragma unroll
@@ -725,7 +725,7 @@ __global__ __launch_bounds__(BIG_WAVES * 64, 1) void gemm_big_kernel(
         float y[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          y[r] = rbf(silu_f(rbf(acc[nt][mt][r]))) * rbf(acc[nt + NT / 2][mt][r]);
+          y[r] = silu_rbf(rbf(acc[nt][mt][r])) * rbf(acc[nt + NT / 2][mt][r]);
         *reinterpret_cast<uint2*>(out + m * out_stride + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
       }
     } else {
@@ -763,7 +763,14 @@ __global__ __launch_bounds__(BIG_WAVES * 64, 1) void gemm_big_kernel(
 // qkv 22.7 -> 20.3 us with the tiled kernel's split counts; stages of 32 in 7-8 buffers (twice
 // the bytes in flight, twice the barriers) were slower (8.16 against 7.19 ms per verify).
 constexpr int RW_MAXM = 256;                // activation rows per workgroup at most (8 waves x 32)
-constexpr int RW_NBUF = 3;
+#ifndef QD_RW_NBUF_MAX
+#define QD_RW_NBUF_MAX 3
+#endif
+constexpr int RW_LDS_BYTES = 160 * 1024;
+// stage buffers for `rows` staged rows (128 bytes each): as many as fit the CU's LDS, 3..max
+__host__ __device__ constexpr int rw_nbuf(int rows) {
+  return RW_LDS_BYTES / (rows * 128) > QD_RW_NBUF_MAX ? QD_RW_NBUF_MAX : RW_LDS_BYTES / (rows * 128);
+}
 
 template <int EPI, bool SPLIT, int NT, int MT>
 __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
@@ -777,6 +784,8 @@ __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
   constexpr int ROWS = WR + RM;              // staged rows per stage (weights, then activations)
   constexpr int NBLK = ROWS / 8;             // 1 KiB load blocks per stage (8 rows x 128 bytes)
   constexpr int PER = (NBLK + 7) / 8;        // loads per wave per stage (the last wraps around)
+  constexpr int RW_NBUF = rw_nbuf(ROWS);
+  static_assert(RW_NBUF >= 3 && RW_NBUF * ROWS * 128 <= RW_LDS_BYTES, "stage buffers");
   __shared__ uint4 sm[RW_NBUF][ROWS * 8];
   // workgroup -> (weight block, K split, activation half): the halves of one weight block are
   // workgroups g and g + 8 (dispatch puts workgroup g on XCD g % 8), so they share an L2
@@ -887,7 +896,7 @@ __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
         float y[4];
         if constexpr (SW) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) y[r] = rbf(silu_f(rbf(acc[t][mt][r]))) * rbf(acc[NT + t][mt][r]);
+          for (int r = 0; r < 4; ++r) y[r] = silu_rbf(rbf(acc[t][mt][r])) * rbf(acc[NT + t][mt][r]);
         } else if constexpr (EPI == EPI_RES) {
           const uint2 rv = *reinterpret_cast<const uint2*>(res + m * res_stride + n);
           y[0] = bflo(rv.x) + rbf(acc[t][mt][0]);
@@ -1090,7 +1099,7 @@ int gemm_rows_query(int64_t M, int64_t N, int64_t K, int epi, bool partials_only
   out[4] = P.splits;
   out[5] = P.ks_per;
   out[6] = P.mh > 1 ? (nblk + 7) / 8 * 8 * P.mh : nblk;             // grid (launch_rows)
-  out[7] = (int64_t)RW_NBUF * (16 * wt + 128 * P.mt) * 128;          // static LDS bytes
+  out[7] = (int64_t)rw_nbuf(16 * wt + 128 * P.mt) * (16 * wt + 128 * P.mt) * 128;   // static LDS bytes
   return 1;
 }
 

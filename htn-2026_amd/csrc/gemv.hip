@@ -111,7 +111,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(const bf16_t* __restrict_
       if constexpr (EPI == EPI_RES) {
         y = bf2f(res[b * res_stride + n]) + rbf(ag[b]);
       } else if constexpr (SW) {
-        y = rbf(silu_f(rbf(ag[b]))) * rbf(au[b]);
+        y = silu_rbf(rbf(ag[b])) * rbf(au[b]);
       } else {
         y = ag[b];
       }

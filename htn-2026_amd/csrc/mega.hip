@@ -411,7 +411,7 @@ __device__ void phase_o_gu(const MegaParams& p, Smem& sm, int l, int wg, int P, 
       const float ag = mg_dot<5>(g[rr % 3], sm.xs);
       const float au = mg_dot<5>(u[rr % 3], sm.xs);
       if (rr + 3 < RW) load_gu(rr % 3, rr + 3);
-      if ((hw_tid() & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(rbf(silu_f(rbf(ag))) * rbf(au));
+      if ((hw_tid() & 63) == 0) sm.obuf[k] = (uint16_t)f2bf(silu_rbf(rbf(ag)) * rbf(au));
     }
   }
   lds_barrier();

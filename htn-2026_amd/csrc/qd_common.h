@@ -117,6 +117,23 @@ __device__ __forceinline__ uint4 norm8(const uint4 v, const uint4 g, float rstd)
 // torch silu in fp32 opmath: x / (1 + exp(-x)) (HIP's own expf, IEEE divide)
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
+// bf16(silu_f(g)), the only form the SwiGLU paths use, at a fraction of its cost.  The quotient
+// q = g * rcp(1 + exp2(-g log2 e)) on the hardware exp2 and reciprocal (each within 1 ulp)
+// differs from silu_f's by at most 21 x 2^-23 relative for |g| <= 16: the exponent's rounding
+// carries |g| x 2^-23 into exp, the two hardware ops 2^-23 each, the roundings of t, d and q
+// the rest, and silu_f's own expf and roundings 2 x 2^-23.  That is at most 42 fp32 ulps
+// (adjacent bit patterns), so the two round to the same bf16 unless q's low 16 bits lie within
+// 64 of 0x8000 (a bf16 rounding midpoint).  Those inputs (~0.2 % of them), |g| > 16, infinities
+// and NaN take silu_f itself, so the result is silu_f's bf16 for every g
+// (tests/test_gpu_kernels.py checks all 65,536 bf16 inputs against the table of silu_f's).
+__device__ __forceinline__ float silu_rbf(float g) {
+  const float d = 1.0f + __builtin_amdgcn_exp2f(-g * 1.44269504f);
+  const float q = g * __builtin_amdgcn_rcpf(d);
+  const uint32_t m = (__float_as_uint(q) & 0xffffu) - (0x8000u - 64u);   // <= 128: near a midpoint
+  if (__builtin_expect(!(fabsf(g) <= 16.0f) || m <= 128u, 0)) return rbf(silu_f(g));
+  return rbf(q);
+}
+
 // rsqrt(mean + eps) as torch computes it on the CPU: 1 / sqrt(v), each correctly rounded
 __device__ __forceinline__ float rstd_of(float sumsq, int n, float eps) {
   return 1.0f / sqrtf(sumsq / (float)n + eps);

@@ -170,7 +170,7 @@ __device__ __forceinline__ void skinny_block(uint4* lds, const bf16_t* __restric
 #pragma unroll
         for (int w = 1; w < SK_WAVES; ++w) u += red[((w * WT + NT + t) * MT + mt) * 64 + ln];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) y[r] = rbf(silu_f(rbf(v[r]))) * rbf(u[r]);
+        for (int r = 0; r < 4; ++r) y[r] = silu_rbf(rbf(v[r])) * rbf(u[r]);
       } else if constexpr (EPI == EPI_RES) {
         const uint2 rv = *reinterpret_cast<const uint2*>(res + m * rs + n);
         y[0] = bflo(rv.x) + rbf(v[0]);

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_ulp, bf16_ulp
+from helpers import GOLDEN, assert_ulp, bf16_ulp
 from oracle import qwen3_ref as R
 from oracle import synth
 
@@ -153,6 +153,21 @@ def test_swiglu(ops, B):
     out = ops.swiglu(gu.to(DEV))
     sync()
     assert_ulp(out.cpu(), R.swiglu(gu[:, :9728], gu[:, 9728:]), 2, "swiglu")
+
+
+def test_silu_every_bf16_input(ops):
+    """bf16(silu(g)) over the whole domain -- all 65,536 bf16 bit patterns g -- equals the table
+    recorded from the IEEE evaluation (tests/golden/record_silu_table.py; the CPU suite pins the
+    table to the oracle's silu bit for bit), so the SwiGLU paths' cheaper evaluation with its
+    near-midpoint fallback changes no result."""
+    import sys
+    sys.path.insert(0, GOLDEN)
+    from record_silu_table import silu_table
+    say("silu over all 65536 bf16 inputs against the recorded table")
+    want = np.load(os.path.join(GOLDEN, "silu_bf16.npy"))
+    got = silu_table(torch.device(DEV))
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} inputs differ, first {[hex(int(x)) for x in bad[:8]]}"
 
 
 # ------------------------------------------------------------------ projections

@@ -127,6 +127,20 @@ def test_swiglu_golden():
     assert torch.equal(R.swiglu(z, torch.ones(4, dtype=torch.bfloat16)), z)
 
 
+def test_silu_table_is_the_oracles_silu():
+    """tests/golden/silu_bf16.npy (bf16(silu(g)) for every bf16 bit pattern g, recorded on the
+    GPU from the IEEE evaluation) equals the oracle's swiglu with the up half 1 over the whole
+    domain: the same bits for every finite g, NaN where the oracle gives NaN (silu(-inf))."""
+    tab = np.load(os.path.join(GOLDEN, "silu_bf16.npy"))
+    assert tab.shape == (65536,) and tab.dtype == np.uint16
+    g = R.bits_to_bf16(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    want = R.swiglu(g, torch.ones_like(g)).float()
+    got = R.bits_to_bf16(tab).float()
+    both_nan = torch.isnan(want) & torch.isnan(got)
+    assert bool(((want == got) | both_nan).all())
+    assert int(torch.isnan(want).sum()) == 255          # the NaN patterns and silu(-inf)
+
+
 def test_attention_golden():
     od = R.attention(T("sd_q"), T("sd_k"), T("sd_v"), torch.ones((1, 1, 1, 37), dtype=torch.bool))
     assert_ulp(od, T("sd_o"), 2, "decode sdpa", abs_floor=2 ** -10)
