@@ -211,7 +211,8 @@ class Engine:
     def _decide_tree(self, sh, ids, n):
         """The warmup gate (engine.py:910-936): n tokens with tree speculation and n plain on
         the same buffers; keep trees only if they emit exactly the plain greedy ids and take
-        less than TREE_MIN_GAIN of the plain wall time (best of two runs each)."""
+        less than TREE_MIN_GAIN of the plain wall time (best of two runs each, timed only when
+        the ids agree: otherwise trees are off whatever their speed)."""
         def run(tree):
             t0 = time.perf_counter()
             it = (_tree.stream_tree(self, sh, ids, n, _draft.LookaheadDrafter()) if tree
@@ -221,13 +222,14 @@ class Engine:
         plain, _ = run(False)
         tree, _ = run(True)
         exact = tree == plain
-        ms_tree = min(run(True)[1] for _ in range(2)) * 1e3
-        ms_plain = min(run(False)[1] for _ in range(2)) * 1e3
+        acc = (self.tree_stats or {}).get("accepted") or [1]
+        ms_tree = ms_plain = None
+        if exact:                  # the timing only chooses between two paths with the same ids
+            ms_tree = round(min(run(True)[1] for _ in range(2)) * 1e3, 3)
+            ms_plain = round(min(run(False)[1] for _ in range(2)) * 1e3, 3)
         on = exact and ms_tree < TREE_MIN_GAIN * ms_plain
-        stats = self.tree_stats or {}
-        acc = stats.get("accepted") or [1]
         self.tree_log[(sh.B, sh.S, sh.N)] = {
-            "tokens": n, "exact": exact, "tree_ms": round(ms_tree, 3), "plain_ms": round(ms_plain, 3),
+            "tokens": n, "exact": exact, "tree_ms": ms_tree, "plain_ms": ms_plain,
             "accept_mean": round(sum(acc) / len(acc), 3), "T": sh.tree_T, "on": on}
         return on
 
