@@ -5,8 +5,9 @@
 
 Workloads (the benchmark's configurations 2-5; configuration 1 is the CPU parity case):
   value  config 3 -- 36 layers, B=1, prompt 512, up to 256 new tokens: decode tok/s over K timed
-         steps (one step = one hipGraph replay of the whole decode step: embed, 36 layers,
-         LM head + argmax), after W warm-up steps; inputs resident in HBM.
+         steps (one step = the whole decode step -- embed, 36 layers, LM head + argmax --
+         as one launch of the persistent kernel, or one hipGraph replay of the per-launch
+         step with QD_MEGA=0), after W warm-up steps; inputs resident in HBM.
   b32    config 4 -- 36 layers, B=32, prompts of 2048, up to 128 new tokens (same method).
   tree   config 5 -- tree verification, B=4, context 8192, 64-node random trees: the verify
          forward timed with HIP events (bytes/s and MFMA TFLOP/s), plus an end-to-end

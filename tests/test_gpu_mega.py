@@ -92,6 +92,7 @@ def test_mega_graph_replay_36_layers(mods):
     stream, kv_a, kv_b = _prefilled_pair(M, _lib, model, S, M.kv_capacity(S, N), seed=7)
     ra = M.DecodeRunner(kv_a, stream, mega=False)
     rb = M.DecodeRunner(kv_b, stream, mega=True)
+    rb.direct = False                # replay the captured one-node graph, not a direct launch
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
         ra.capture()
