@@ -763,6 +763,10 @@ __global__ __launch_bounds__(BIG_WAVES * 64, 1) void gemm_big_kernel(
 // qkv 22.7 -> 20.3 us with the tiled kernel's split counts; stages of 32 in 7-8 buffers (twice
 // the bytes in flight, twice the barriers) were slower (8.16 against 7.19 ms per verify).
 constexpr int RW_MAXM = 256;                // activation rows per workgroup at most (8 waves x 32)
+// Stage buffers: three (two stages in flight).  Four or five, which the LDS holds for every
+// instantiation here, measured slower on a config-5 verify (6.56 / 6.60 against 6.51 ms): the
+// loop's DMA, LDS reads and MFMAs each take about as long as the whole loop (timing copies),
+// so deeper prefetch only adds LDS traffic.
 #ifndef QD_RW_NBUF_MAX
 #define QD_RW_NBUF_MAX 3
 #endif
