@@ -1113,8 +1113,6 @@ int64_t gemm_tile_ws_floats(int64_t M, int64_t N, int64_t K, int epi) {
   return sp > 1 ? (int64_t)sp * M * N : 0;
 }
 
-int64_t gemm_tile_argmax_parts(int64_t N) { return N / TN; }
-
 int gemm_tile_partials(const bf16_t* x, int64_t xs, int64_t M, const bf16_t* w, int64_t N,
                        int64_t K, float* part, int64_t part_floats, hipStream_t s) {
   if (M < GEMM_TILE_MIN_M || !part ||
