@@ -41,7 +41,7 @@ static_assert(TILE_RING % 2 == 0, "the ring slots and the two LDS buffers advanc
 #endif
 constexpr int TILE_GROUP_M = QD_TILE_GROUP_M;
 #ifndef QD_BIG_GROUP_M
-#define QD_BIG_GROUP_M 8
+#define QD_BIG_GROUP_M 4  // 256 x 256 tiles: 4 M blocks per group (8: 1-4 % slower at 32768 rows)
 #endif
 constexpr int BIG_GROUP_M = QD_BIG_GROUP_M;
 #ifndef QD_TILE8
@@ -513,22 +513,18 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
 // tile order) and keeps the MFMA pipe 30 % busy.  This kernel doubles the tile both ways, halving
 // the traffic per flop: a workgroup of 8 waves (two per SIMD) owns 256 weight rows x 256
 // activation rows, wave (wm, wn) the 128 activation rows 128 wm .. x the 64 weight rows 64 wn ..
-// (4 x 8 MFMA tiles, 128 fp32 accumulators per lane).  K advances in stages of 32 that go from
+// (4 x 8 MFMA tiles, 128 fp32 accumulators per lane).  K advances in stages of 64 that go from
 // global memory straight into LDS (global_load_lds_dwordx4: no staging registers, no LDS store
-// instructions), BIG_NBUF stage buffers of 32 KiB with BIG_NBUF - 1 stages in flight: with the
-// loads staged through registers only one 64-deep stage fitted in flight, and a copy of that
-// kernel without its MFMAs (loads, LDS stores and barriers only) took 539 us of the full
-// kernel's 714 us for a 6144-row gate/up -- bound by the load round trip, not the MFMA pipe.
+// instructions), two stage buffers of 64 KiB.  Each load instruction fetches whole 128-byte
+// lines (8 rows x 128 bytes): with stages of 32 (16 rows x 64 bytes per instruction, half lines)
+// the same kernel ran 6-10 % slower, and a timing copy whose loads all hit one L1 line ran 25-30
+// % faster than either -- the cost is in the L1/L2 request stream, not in the LDS writes.  (With
+// the loads staged through registers only one 64-deep stage fitted in flight, and a copy of that
+// kernel without its MFMAs took 539 us of the full kernel's 714 us for a 6144-row gate/up.)
 // SwiGLU: a wave's 64 weight rows are 32 gate rows and the 32 up rows of the same outputs.
 constexpr int BT = 256;                      // weight rows and activation rows per workgroup
-constexpr int BK = 32;                       // K per stage: 64 bytes of every row
-#ifndef QD_BIG_NBUF
-#define QD_BIG_NBUF 4
-#endif
-constexpr int BIG_NBUF = QD_BIG_NBUF;        // LDS stage buffers (BIG_NBUF x 32 KiB <= 160 KiB)
-static_assert(BIG_NBUF >= 2 && BIG_NBUF <= 5, "stage buffers");
+constexpr int BK = 64;                       // K per stage: 128 bytes of every row
 
-// LDS byte address of a __shared__ object
 // 8 waves (two per SIMD), two along the activation rows and four along the weight rows: wave
 // (wm, wn) owns activation rows 128 wm .. and weight rows 64 wn .. (8 x 4 MFMA tiles, 128 fp32
 // accumulators per lane).  SwiGLU: a wave's 64 weight rows are 32 gate rows and the 32 up rows
@@ -546,12 +542,12 @@ __global__ __launch_bounds__(BIG_WAVES * 64, 1) void gemm_big_kernel(
   constexpr int NT = BT / WN / 16;           // MFMA tiles per wave along the weight rows
   constexpr int HALF = NT * 8;               // SwiGLU: gate rows per wave
   constexpr int ROWS = BT / WAVES;           // LDS rows of each tile a wave loads per stage
-  constexpr int BLK = ROWS / 16;             // ... as 1 KiB blocks of 16 rows
-  constexpr int PER = 2 * BLK;               // loads per wave per stage
-  // [stage buffer][weights, activations][row * 4 + position]: row r's 64 bytes hold its four
-  // 16-byte K units, unit u at position u ^ ((r / 2) % 4), so that the 8 lanes of a fragment
-  // read (rows c .. c + 7, one unit each) cover all 128 bytes of the banks
-  __shared__ uint4 sm[BIG_NBUF][2][BT * 4];
+  constexpr int BLK = ROWS / 8;              // ... as 1 KiB blocks of 8 rows (one load each)
+  static_assert(NT == 4 && BLK == 4, "the step below interleaves 4 x 2 loads with 4 x 8 MFMAs");
+  // [stage buffer][weights, activations][row * 8 + position]: row r's 128 bytes hold its eight
+  // 16-byte K units, unit u at position u ^ (r % 8), so that the 8 lanes of a fragment read
+  // (rows c .. c + 7, one unit each) cover all 128 bytes of the banks
+  __shared__ uint4 sm[2][2][BT * 8];
   const int total = gridDim.x, h = blockIdx.x;
   const int xq = total >> 3, xr = total & 7, xcd = h & 7, slot = h >> 3;
   const int L = xcd < xr ? xcd * (xq + 1) + slot : xr * (xq + 1) + (xcd - xr) * xq + slot;
@@ -566,7 +562,7 @@ __global__ __launch_bounds__(BIG_WAVES * 64, 1) void gemm_big_kernel(
   const int c = lane & 15, q = lane >> 4;
   const int wn = wave % WN, wm = wave / WN;
   const int64_t m0 = (int64_t)mb * BT;
-  const int ksteps = K / BK;
+  const int stages = K / BK;
   // weight row of LDS row r: plain nb*256 + r; SwiGLU: LDS rows [2 HALF j, 2 HALF j + HALF) are
   // the gate rows of outputs nb*128 + HALF j .., the next HALF the up rows (+ N) of the same outputs
   auto wrow = [&](int r) -> int64_t {
@@ -583,80 +579,93 @@ __global__ __launch_bounds__(BIG_WAVES * 64, 1) void gemm_big_kernel(
     const int64_t m = m0 + r;
     return m < M ? m : M - 1;
   };
-  // loads: wave v fills LDS rows ROWS v .. of both tiles as BLK 1 KiB blocks of 16 rows; lane l
-  // of a block writes position l % 4 of row l / 4, i.e. K unit (l % 4) ^ ((row / 2) % 4)
-  const int unit = (lane & 3) ^ ((lane >> 3) & 3);
+  // loads: wave v fills LDS rows ROWS v .. of both tiles as BLK 1 KiB blocks of 8 rows; lane l
+  // of a block writes position l % 8 of row l / 8 (row % 8 = l / 8), i.e. K unit (l % 8) ^ (l / 8)
+  const int unit = (lane & 7) ^ (lane >> 3);
   uint32_t wof[BLK], xof[BLK];
 #pragma unroll
   for (int j = 0; j < BLK; ++j) {
-    const int r = ROWS * wave + 16 * j + (lane >> 2);
+    const int r = ROWS * wave + 8 * j + (lane >> 3);
     wof[j] = (uint32_t)(wrow(r) * K * 2 + unit * 16);
     xof[j] = (uint32_t)(xrow(r) * x_stride * 2 + unit * 16);
   }
-  const uint32_t lbase = __builtin_amdgcn_readfirstlane(lds_u32(&sm[0][0][0])) + wave * ROWS * 64;
-  auto issue = [&](int ks, int buf) {
-    const char* wb = reinterpret_cast<const char*>(W) + (size_t)ks * (BK * 2);
-    const char* xb = reinterpret_cast<const char*>(X) + (size_t)ks * (BK * 2);
-    const uint32_t l = lbase + (uint32_t)buf * (2 * BT * 4 * 16);
-#pragma unroll
-    for (int j = 0; j < BLK; ++j) dma16(wb, wof[j], l + 1024 * j);
-#pragma unroll
-    for (int j = 0; j < BLK; ++j) dma16(xb, xof[j], l + BT * 4 * 16 + 1024 * j);
+  const uint32_t lbase = __builtin_amdgcn_readfirstlane(lds_u32(&sm[0][0][0])) + wave * ROWS * 128;
+  constexpr uint32_t XOFF = BT * 8 * 16, BUF = 2 * XOFF;   // activation tile, stage buffer (bytes)
+  // load i (0..7) of stage st into buffer b: weights 0..3, activations 4..7
+  auto load = [&](int st, int b, int i) {
+    const char* base = reinterpret_cast<const char*>(i < BLK ? (const void*)W : (const void*)X) +
+                       (size_t)st * (BK * 2);
+    const int j = i % BLK;
+    dma16(base, i < BLK ? wof[j] : xof[j], lbase + (uint32_t)b * BUF + (i < BLK ? 0u : XOFF) + 1024u * j);
   };
   f32x4_t acc[NT][8];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int u = q ^ ((c >> 1) & 3);
-  const int fa = (NT * 16 * wn + c) * 4 + u, fb = (128 * wm + c) * 4 + u;  // + 64 t: rows + 16 t
-  // fragments of one stage: NT weight tiles, 8 activation tiles (one 16-byte unit per lane each)
+  // fragment of K half hf (units 4 hf .. 4 hf + 3) of a 16-row tile: lane (c, q) reads unit
+  // 4 hf + q of row tile + c, at position (4 hf + q) ^ (c % 8); tiles are 16 rows = 128 uint4 apart
+  const int pa0 = (64 * wn + c) * 8, pb0 = (128 * wm + c) * 8;
+  const int u0 = q ^ (c & 7), u1 = (4 + q) ^ (c & 7);
+  // fragments of one K half: NT weight tiles, 8 activation tiles (one 16-byte unit per lane each)
   struct Frag {
     uint4 a[NT], b[8];
   };
-  auto read = [&](Frag& f, int buf) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) f.a[t] = sm[buf][0][fa + 64 * t];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) f.b[t] = sm[buf][1][fb + 64 * t];
+  // read fragment t (0..11: weight tiles 0..3, then activation tiles 0..7) of half hf of buffer b
+  auto rd = [&](Frag& f, int b, int hf, int t) {
+    const int u = hf ? u1 : u0;
+    if (t < NT) f.a[t] = sm[b][0][pa0 + 128 * t + u];
+    else f.b[t - NT] = sm[b][1][pb0 + 128 * (t - NT) + u];
   };
-  auto mma = [&](const Frag& f) {
+  // Sub-step j contracts K half j (stage j / 2) from registers while the fragments of half j + 1
+  // are read, in four groups of (two loads, three fragment reads, eight MFMAs) so the load and
+  // LDS instructions issue between MFMAs.  Stage s lives in buffer s % 2.  Odd sub-steps read the
+  // next stage: they first wait for this wave's loads (all of them: stage s + 1 is the only one
+  // in flight) and meet the other waves at a barrier, after which every wave's stage s + 1 has
+  // landed and every wave has read stage s out of its buffer, which then takes stage s + 2 (the
+  // loads of that sub-step).  One barrier per stage.
+  auto sub = [&](int s, int hf, const Frag& cur, Frag& nxt) {
+    const int b = s & 1;
+    const bool ld = hf && s + 2 < stages, rdn = !hf || s + 1 < stages;
+    const int rb = hf ? b ^ 1 : b;
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
+    for (int g = 0; g < 4; ++g) {
+      if (ld) {
+        load(s + 2, b, 2 * g);
+        load(s + 2, b, 2 * g + 1);
+      }
+      if (rdn) {
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(f.a[nt]), as_bf8(f.b[mt]),
-                                                              acc[nt][mt], 0, 0, 0);
+        for (int t = 3 * g; t < 3 * g + 3; ++t) rd(nxt, rb, hf ^ 1, t);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int mt = 2 * g; mt < 2 * g + 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(cur.a[nt]), as_bf8(cur.b[mt]),
+                                                                acc[nt][mt], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
-  // Stage s lives in buffer s % BIG_NBUF.  Step ks contracts stage ks from registers while the
-  // fragments of stage ks + 1 are read: at its top this wave's loads of stage ks + 1 have landed
-  // once at most min(BIG_NBUF - 2, stages after it) stages of its loads are outstanding, and after
-  // the barrier every wave's have, and every wave has read stage ks out of its buffer, which then
-  // takes stage ks + BIG_NBUF.
-  const int nb_ = BIG_NBUF;
 #pragma unroll
-  for (int s = 0; s < BIG_NBUF; ++s)
-    if (s < ksteps) issue(s, s);
-  Frag f0, f1;
-  wait_stages<PER, BIG_NBUF - 1>(ksteps - 1);
+  for (int i = 0; i < 2 * BLK; ++i) load(0, 0, i);
+  if (stages > 1) {
+#pragma unroll
+    for (int i = 0; i < 2 * BLK; ++i) load(1, 1, i);
+    wait_vm<2 * BLK>();                        // stage 0 landed (stage 1 still in flight)
+  } else {
+    wait_vm<0>();
+  }
   lds_barrier();
-  read(f0, 0);
-  // every step has the barrier and the reads (the last step's reads fetch a stage buffer that
-  // is never contracted): the MFMAs of a step then follow a barrier on every path, so the
-  // compiler knows that the current fragments have arrived and waits only for them
-  auto step = [&](int ks, Frag& cur, Frag& nxt) {
-    const int buf = ks % nb_;
-    wait_stages<PER, BIG_NBUF - 2>(ksteps - 2 - ks);
+  Frag f0, f1;
+#pragma unroll
+  for (int t = 0; t < NT + 8; ++t) rd(f0, 0, 0, t);
+  for (int s = 0; s < stages; ++s) {
+    sub(s, 0, f0, f1);
+    wait_vm<0>();
     lds_barrier();
-    if (ks + BIG_NBUF < ksteps) issue(ks + BIG_NBUF, buf);
-    read(nxt, buf + 1 < BIG_NBUF ? buf + 1 : 0);
-    __builtin_amdgcn_sched_barrier(0);       // the reads go out ahead of the MFMAs
-    mma(cur);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  for (int ks = 0; ks < ksteps; ks += 2) {
-    step(ks, f0, f1);
-    if (ks + 1 < ksteps) step(ks + 1, f1, f0);
+    sub(s, 1, f1, f0);
   }
 
   // epilogue: lane (c, q) of acc[nt][mt] holds weight rows 4 q + r of tile nt = output columns
