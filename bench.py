@@ -1,7 +1,7 @@
 """Decode benchmark on one MI355X: Qwen3-4B-shaped bf16 greedy decode through the HIP engine.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-b32] [--no-tree] [--no-cpu]
-                    [--no-layer] [--no-api]
+                    [--no-layer] [--no-api] [--no-gemm]
 
 Workloads (the benchmark's configurations 2-5; configuration 1 is the CPU parity case):
   value  config 3 -- 36 layers, B=1, prompt 512, up to 256 new tokens: decode tok/s over K timed
@@ -21,6 +21,9 @@ Workloads (the benchmark's configurations 2-5; configuration 1 is the CPU parity
   layer_kernels_large  the same four kernels at row counts that move >= 100 MB per launch
          (where bandwidth, not launch latency, binds): GB/s, fraction of 8 TB/s, and a device
          copy of the same bytes as the read+write yardstick.
+  prefill_gemm  the four projections of a prefill chunk (32768 rows, the engine's chunk) through
+         qd_linear (the 256 x 256-tile MFMA kernel) and, beside them, torch.matmul (hipBLASLt)
+         on the same operands: us per launch and TFLOP/s against the 2.5 PFLOP/s bf16 dense peak.
   step_ms  per-step spread (median, p90, min, max) of the same K steps replayed again with an
          event after each step (the headline timing has no events between steps).
 Weights are seeded random-init N(0, 0.02) generated on the device; prompt ids uniform.
@@ -49,6 +52,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "htn-2026_amd"))
 
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0
 # HBM bytes per gate/up launch at B=1, from two rocprofv3 --pmc passes over this script
 # (`--calib-copy-mib 512`): FETCH_SIZE 48,703.0 KiB x 1.99986 + WRITE_SIZE 38.0 KiB x 1.0, the
 # factors being what the same counters read for a 512 MiB device copy.  Summary and commands:
@@ -516,6 +520,51 @@ def layer_kernels_large(reps=20, scale=1):
     return out
 
 
+def prefill_gemm(rows=32768, reps=20):
+    """The four projections at a prefill chunk's row count through qd_linear (RMSNorm-free
+    operands: the GEMM alone) and torch.matmul (hipBLASLt) on the same operands; synthetic bf16
+    N(0, 1) activations, N(0, 0.02) weights.  HIP events on the current stream (the one both
+    calls launch on) around `reps` back-to-back launches after 5 warm-up launches."""
+    import torch
+    from qdecode import ops
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(21)
+    shapes = [("qkv", 6144, 2560, ops.EPI_NONE), ("o", 2560, 4096, ops.EPI_NONE),
+              ("gate_up_swiglu", 2 * 9728, 2560, ops.EPI_SWIGLU), ("down", 2560, 9728, ops.EPI_NONE)]
+
+    def timed(fn):
+        for _ in range(5):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    out = []
+    for name, n_w, K, epi in shapes:
+        x = torch.randn(rows, K, device=dev, dtype=torch.bfloat16, generator=g)
+        w = torch.randn(n_w, K, device=dev, dtype=torch.bfloat16, generator=g) * 0.02
+        y = torch.empty(rows, n_w // 2 if epi == ops.EPI_SWIGLU else n_w, device=dev,
+                        dtype=torch.bfloat16)
+        yb = torch.empty(rows, n_w, device=dev, dtype=torch.bfloat16)
+        flop = 2.0 * rows * n_w * K
+        need = ops._lib.LIB.qd_linear_workspace_bytes(rows, y.shape[1], K, 0)
+        ws = ops.workspace(need, dev) if need else None
+        us = timed(lambda: ops.linear(x, w, epi, out=y, ws=ws))
+        ub = timed(lambda: torch.matmul(x, w.t(), out=yb))
+        out.append({"gemm": name, "rows": rows, "n": n_w, "k": K, "us_per_launch": round(us, 1),
+                    "tflops": round(flop / us / 1e6, 1),
+                    "frac": round(flop / us / 1e6 / PEAK_BF16_TFLOPS, 4),
+                    "hipblaslt_us": round(ub, 1), "hipblaslt_tflops": round(flop / ub / 1e6, 1)})
+        del x, w, y, yb, ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(budget_s=15.0, prompt_len=512):
     """The CPU oracle (torch CPU, oneDNN bf16) on the same 36-layer architecture and
     generator: prefill config 3's 512-token prompt (untimed), then time greedy decode steps for
@@ -622,6 +671,7 @@ def main():
     ap.add_argument("--no-tree", action="store_true")
     ap.add_argument("--no-layer", action="store_true", help="skip the config-2 kernel microbench")
     ap.add_argument("--no-api", action="store_true", help="skip the Engine.generate runs")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM comparison")
     ap.add_argument("--tree-steps", type=int, default=20, help="timed verify forwards")
     ap.add_argument("--tree-e2e", type=int, default=256, help="tokens of the end-to-end tree run")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -732,6 +782,17 @@ def main():
         eng.shape = None
         torch.cuda.empty_cache()
 
+    pgemm = None
+    if not a.no_gemm:
+        eng.shape = None
+        torch.cuda.empty_cache()
+        pgemm = prefill_gemm()
+        for c in pgemm:
+            log(f"prefill GEMM {c['gemm']:>14}: {c['us_per_launch']:.1f} us, {c['tflops']:.0f} "
+                f"TFLOP/s ({c['frac']:.3f} of 2.5 PF); hipBLASLt {c['hipblaslt_us']:.1f} us, "
+                f"{c['hipblaslt_tflops']:.0f} TFLOP/s")
+        torch.cuda.empty_cache()
+
     cpu = cpu_more = None
     if not a.no_cpu:
         eng = None
@@ -782,6 +843,7 @@ def main():
         "prefill_s": round(r1["prefill_s"], 3),
         "b32": b32,
         "tree": tree,
+        "prefill_gemm": pgemm,
         "layer_kernels": layer,
         "layer_kernels_large": layer_large,
         "api": api,
