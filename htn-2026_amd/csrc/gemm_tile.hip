@@ -796,7 +796,7 @@ __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
   constexpr int RM = 128 * MT;               // staged activation rows
   constexpr int ROWS = WR + RM;              // staged rows per stage (weights, then activations)
   constexpr int NBLK = ROWS / 8;             // 1 KiB load blocks per stage (8 rows x 128 bytes)
-  constexpr int PER = (NBLK + 7) / 8;        // loads per wave per stage (the last wraps around)
+  constexpr int PER = (NBLK + 7) / 8;        // loads per wave per stage (at most)
   constexpr int RW_NBUF = rw_nbuf(ROWS);
   static_assert(RW_NBUF >= 3 && RW_NBUF * ROWS * 128 <= RW_LDS_BYTES, "stage buffers");
   __shared__ uint4 sm[RW_NBUF][ROWS * 8];
@@ -831,8 +831,12 @@ __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
     const int xm = min(m0 + r - WR, M - 1);
     return (uint32_t)((int64_t)xm * x_stride * 2);
   };
-  // wave w loads blocks w, w + 8, ... (mod NBLK); lane l of a block: row l / 8, position l % 8,
-  // K unit (l % 8) ^ (row % 8)
+  // wave w loads blocks w, w + 8, ... < NBLK (PER of them, or PER - 1 where NBLK is not a
+  // multiple of 8: repeating blocks to even the waves out cost 10-12 % more load requests, the
+  // stream this loop is bound by); lane l of a block: row l / 8, position l % 8, K unit
+  // (l % 8) ^ (row % 8)
+  static_assert(PER >= 2, "PER - 1 loads for the short waves");
+  const bool full = wave + 8 * (PER - 1) < NBLK;   // uniform per wave
   uint32_t voff[PER];
   int blk[PER];
 #pragma unroll
@@ -842,13 +846,15 @@ __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
     voff[j] = grow_off(r) + (uint32_t)(((lane & 7) ^ ((lane >> 3) & 7)) * 16);
   }
   const uint32_t lbase = __builtin_amdgcn_readfirstlane(lds_u32(&sm[0][0]));
-  auto issue = [&](int ks, int buf) {
+  // loads j0 .. j1 - 1 of this wave's PER (or PER - 1) for stage ks into buffer buf
+  auto issue = [&](int ks, int buf, int j0 = 0, int j1 = 1 << 30) {
     const char* wb = reinterpret_cast<const char*>(W) + (size_t)ks * (TK * 2);
     const char* xb = reinterpret_cast<const char*>(X) + (size_t)ks * (TK * 2);
     const uint32_t l = lbase + (uint32_t)buf * (ROWS * 128);
 #pragma unroll
     for (int j = 0; j < PER; ++j)
-      dma16(blk[j] * 8 < WR ? wb : xb, voff[j], l + (uint32_t)blk[j] * 1024);
+      if (j >= j0 && j < j1 && (j < PER - 1 || full))
+        dma16(blk[j] * 8 < WR ? wb : xb, voff[j], l + (uint32_t)blk[j] * 1024);
   };
   f32x4_t acc[WT][MT];
 #pragma unroll
@@ -856,10 +862,15 @@ __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const bool active = m0 + 16 * MT * wave < M;   // uniform per wave
-  auto compute = [&](int buf) {
+  // contract the stage in buffer buf as two halves of K = 32, each preceded by half of the loads
+  // of stage ks_next (< 0: none) into buf_next: issued between the MFMAs rather than all ahead of
+  // them, the verify took 6.39 instead of 6.51 ms
+  auto compute = [&](int buf, int ks_next, int buf_next) {
     const uint4* b0 = sm[buf];
 #pragma unroll
     for (int s_ = 0; s_ < 2; ++s_) {
+      if (ks_next >= 0) issue(ks_next, buf_next, s_ ? PER / 2 : 0, s_ ? PER : PER / 2);
+      __builtin_amdgcn_sched_barrier(0);
       const int u_ = (4 * s_ + q) ^ (c & 7);
       uint4 a_[WT], b_[MT];
 #pragma unroll
@@ -875,9 +886,9 @@ __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
     }
   };
   // stage kbeg + i in buffer i % RW_NBUF; at the top of step i this wave's loads of stage i have
-  // landed once at most min(RW_NBUF - 2, stages after it) stages of its loads are outstanding;
-  // after the barrier every wave's have, and every wave is done with stage i - 1, whose buffer
-  // then takes stage i + RW_NBUF - 1
+  // landed once at most min(RW_NBUF - 2, stages after it) stages of its loads (PER or PER - 1 a
+  // stage) are outstanding; after the barrier every wave's have, and every wave is done with
+  // stage i - 1, whose buffer then takes stage i + RW_NBUF - 1
   constexpr int P = RW_NBUF - 1;
   const int nst = kend - kbeg;
 #pragma unroll
@@ -885,10 +896,12 @@ __global__ __launch_bounds__(512, 1) void gemm_rows_kernel(
     if (i < nst) issue(kbeg + i, i);
   int buf = 0;
   for (int i = 0; i < nst; ++i) {
-    wait_stages<PER, P - 1>(nst - 1 - i);
+    if (full) wait_stages<PER, P - 1>(nst - 1 - i);
+    else wait_stages<PER - 1, P - 1>(nst - 1 - i);
     lds_barrier();
-    if (i + P < nst) issue(kbeg + i + P, buf + P < RW_NBUF ? buf + P : buf + P - RW_NBUF);
-    if (active) compute(buf);
+    const int kn = i + P < nst ? kbeg + i + P : -1, bn = buf + P < RW_NBUF ? buf + P : buf + P - RW_NBUF;
+    if (active) compute(buf, kn, bn);
+    else if (kn >= 0) issue(kn, bn);
     buf = buf + 1 < RW_NBUF ? buf + 1 : 0;
   }
 
