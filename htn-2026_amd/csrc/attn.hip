@@ -265,15 +265,20 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
   constexpr uint32_t TILE_B = BA_KT * 16 * 16;                  // bytes of one K (V) tile
   constexpr uint32_t V_OFF = BA_NBUF * TILE_B;                  // sm.v after sm.k
   const int start32 = (int)start, last = (int)cap - 1;
-  auto issue = [&](int it, int buf) {
+  // the tile's K blocks (half 0), its V blocks (half 1), or both (-1)
+  auto issue = [&](int it, int buf, int half = -1) {
     const int ts = start32 + BA_KT * it;
     const uint32_t oa = (uint32_t)min(ts + dk0, last) * 256u + du0;
     const uint32_t ob = (uint32_t)min(ts + dk1, last) * 256u + du1;
     const uint32_t l = lds0 + (uint32_t)buf * TILE_B;
-    dma16(kb, oa, l);
-    dma16(kb, ob, l + 1024u);
-    dma16(vb, oa, l + V_OFF);
-    dma16(vb, ob, l + V_OFF + 1024u);
+    if (half != 1) {
+      dma16(kb, oa, l);
+      dma16(kb, ob, l + 1024u);
+    }
+    if (half != 0) {
+      dma16(vb, oa, l + V_OFF);
+      dma16(vb, ob, l + V_OFF + 1024u);
+    }
   };
   // S' of the tile in `buf` for both row tiles: sc[rt][h] = keys 16 h + 4 q4 .. + 3, row c
   auto scores = [&](int buf, f32x4_t (&sc)[2][4]) {
@@ -422,12 +427,18 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
     const int64_t j0 = start + (int64_t)BA_KT * it;
     return j0 + BA_KT <= open_end && j0 + BA_KT <= kend;
   };
+  // A causal chunk issues a step's V loads after its first phase (the P V update, or for waves
+  // 4-7 softmax + P V) instead of with the K loads: 2596 -> 2548 us per 4 x 8192 layer (two
+  // traced runs each); with ancestor masks (a verify) that measured slower (54.5 -> 55.4 us), so
+  // there all four go first.
+  const bool late_v = anc == nullptr;                        // uniform
   int buf = 0, bprev = BA_NBUF - 1;                          // tiles it and it - 1
   for (int it = 0; it < ntiles; ++it) {
     const int bl = bprev == 0 ? BA_NBUF - 1 : bprev - 1;     // tile it - 2's buffer
-    issue(it + AHEAD, bl);
+    issue(it + AHEAD, bl, late_v ? 0 : -1);
     if (lead) {
       if (it > 0) pv(bprev, pf);
+      if (late_v) issue(it + AHEAD, bl, 1);
       scores(buf, sc);
       if (!whole(it)) mask_tile(start + (int64_t)BA_KT * it, sc);
       softmax(sc, pf);
@@ -437,6 +448,7 @@ __global__ __launch_bounds__(512) void block_attn_mfma_kernel(
         softmax(sc, pf);
         pv(bprev, pf);
       }
+      if (late_v) issue(it + AHEAD, bl, 1);
       scores(buf, sc);
     }
     wait_vm<4 * (AHEAD - 1)>();
