@@ -247,6 +247,38 @@ def test_linear_epilogues(ops, name, B):
         assert bool((d <= bound).all()), f"{name}: max excess {float((d - bound).max())}"
 
 
+# The 256 x 256-tile kernel's shortest pipelines (K = 128: its two K stages both loaded up front;
+# K = 384: six) with a ragged last row block: plain against fp64, residual in place, and SwiGLU
+# bit for bit against the oracle's SwiGLU of the same kernel's own gate and up projections (the
+# gate / up rows reach it through the 64-deep stages' row mapping)
+@pytest.mark.parametrize("K", [128, 384])
+def test_big_tile_short_k(ops, K):
+    M, N = 1100, 512
+    say(f"256 x 256 tiles: M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(77 + K)
+    x = rnd(g, M, K)
+    w = rnd(g, 2 * N, K, scale=0.05)
+    xd, wd = x.to(DEV), w.to(DEV)
+    plain = ops.linear(xd, wd, ops.EPI_NONE)
+    sync()
+    want, acc = exact_linear(x.float(), w.float())
+    assert_ulp(plain.cpu(), want, 2, "plain", abs_floor=2 ** -9)
+    res = rnd(g, M, N, scale=2.0)
+    xo = res.to(DEV).clone()
+    ops.linear(xd, wd[:N].contiguous(), ops.EPI_RES, res=xo, out=xo)
+    sync()
+    want_r = (res.float() + acc[:, :N].float()).to(BF)
+    d = (xo.cpu().float() - want_r.float()).abs()
+    bound = bf16_ulp(acc[:, :N].float()) + 2 * bf16_ulp(torch.maximum(xo.cpu().float().abs(),
+                                                                       want_r.float().abs()))
+    assert bool((d <= bound).all()), f"residual: max excess {float((d - bound).max())}"
+    act = ops.linear(xd, wd, ops.EPI_SWIGLU)
+    sync()
+    pc = plain.cpu()
+    want_s = R.swiglu(pc[:, :N], pc[:, N:])
+    assert torch.equal(act.cpu().view(torch.int16), want_s.view(torch.int16))
+
+
 # ------------------------------------------------------------------ LM head + argmax
 # 1-2 rows: the vector kernel; 3-64: the weight-streaming MFMA kernel (16 / 32 / 64-row
 # activation tiles); 72: the 128 x 128 tiled kernel; 160, 256: the 256 x 256 tile with the argmax
