@@ -247,6 +247,57 @@ def test_linear_epilogues(ops, name, B):
         assert bool((d <= bound).all()), f"{name}: max excess {float((d - bound).max())}"
 
 
+# Ragged shapes across every dispatch range (vector GEMV, skinny MFMA, LDS-staged, all-rows with
+# and without K splits and activation halves, 128 x 128 and 256 x 256 tiles): seeded random
+# (rows, outputs, K, epilogue), against fp64 with test_linear_epilogues' bounds
+_RNG = np.random.default_rng(2024)
+RAGGED = [(int(_RNG.integers(1, 65) if i % 2 else _RNG.integers(65, 1101)),
+           int(_RNG.choice([256, 512, 768, 1280])), int(_RNG.choice([128, 256, 640, 1152])),
+           int(_RNG.integers(0, 3))) for i in range(24)]
+
+
+@pytest.mark.parametrize("M,N,K,epi", RAGGED)
+def test_linear_ragged_shapes(ops, M, N, K, epi):
+    say(f"linear ragged M={M} N={N} K={K} epi={epi}")
+    g = torch.Generator().manual_seed(M * 7919 + N * 31 + K + epi)
+    w = rnd(g, 2 * N if epi == ops.EPI_SWIGLU else N, K, scale=0.05)
+    x = rnd(g, M, K)
+    xd, wd = x.to(DEV), w.to(DEV)
+    if epi == ops.EPI_NONE:
+        out = ops.linear(xd, wd, epi)
+        sync()
+        want, _ = exact_linear(x.float(), w.float())
+        assert_ulp(out.cpu(), want, 2, "plain", abs_floor=2 ** -9)
+    elif epi == ops.EPI_RES:
+        res = rnd(g, M, N, scale=2.0)
+        xo = res.to(DEV).clone()
+        ops.linear(xd, wd, epi, res=xo, out=xo)
+        sync()
+        _, acc = exact_linear(x.float(), w.float())
+        want = (res.float() + acc.float()).to(BF)
+        d = (xo.cpu().float() - want.float()).abs()
+        bound = bf16_ulp(acc.float()) + 2 * bf16_ulp(torch.maximum(xo.cpu().float().abs(),
+                                                                   want.float().abs()))
+        assert bool((d <= bound).all()), f"residual: max excess {float((d - bound).max())}"
+    else:
+        out = ops.linear(xd, wd, epi)
+        sync()
+        _, gate = exact_linear(x.float(), w[:N].float())
+        _, up = exact_linear(x.float(), w[N:].float())
+        want = R.swiglu(gate.float().to(BF), up.float().to(BF))
+        # bf16(gate), bf16(up) may each sit one ulp off the fp64 rounding (fp32 accumulation),
+        # propagated through silu and the product, plus two output ulps
+        gf, uf = gate.float(), up.float()
+        sg = torch.sigmoid(gf)
+        sv = (gf * sg).to(BF).float()
+        dsilu = (sg * (1 + gf * (1 - sg))).abs()
+        got = out.cpu().float()
+        bound = (uf.abs() * (dsilu * bf16_ulp(gf) + bf16_ulp(sv)) + sv.abs() * bf16_ulp(uf)
+                 + 2 * bf16_ulp(torch.maximum(got.abs(), want.float().abs())) + 2 ** -12)
+        d = (got - want.float()).abs()
+        assert bool((d <= bound).all()), f"gate/up: max excess {float((d - bound).max())}"
+
+
 # The 256 x 256-tile kernel's shortest pipelines (K = 128: its two K stages both loaded up front;
 # K = 384: six) with a ragged last row block: plain against fp64, residual in place, and SwiGLU
 # bit for bit against the oracle's SwiGLU of the same kernel's own gate and up projections (the
