@@ -597,6 +597,37 @@ def test_block_attention_causal_chunk_deep(ops):
         assert_ulp(out[b].cpu(), o, 2, f"chunk row {b}", abs_floor=p_round_bound(vc))
 
 
+# Ragged block attention: seeded random batch, block length, cache size and per-row bases, tree
+# (random 4-4-2-2 trees, up to 64 nodes) and causal (up to 300 tokens) -- partial key tiles, partial
+# query blocks, and the launch's own split plan for each shape
+_RNG_BA = np.random.default_rng(4242)
+RAGGED_BA = []
+for _i in range(10):
+    _tree = _i % 2 == 0
+    _B = int(_RNG_BA.integers(1, 4))
+    _T = int(_RNG_BA.integers(1, 65) if _tree else _RNG_BA.integers(1, 301))
+    _cap = int(_RNG_BA.integers(_T + 1, 3001))
+    _bases = [int(_RNG_BA.integers(0, _cap - _T + 1)) for _ in range(_B)]
+    RAGGED_BA.append(("tree" if _tree else "causal", _B, _T, _cap, tuple(_bases)))
+
+
+@pytest.mark.parametrize("mode,B,T,cap,bases", RAGGED_BA)
+def test_block_attention_ragged(ops, mode, B, T, cap, bases):
+    say(f"block_attention ragged {mode}: B={B} T={T} cap={cap} bases {list(bases)}")
+    g = torch.Generator().manual_seed(T * 1009 + cap)
+    q = rnd(g, B, T, 32, 128, scale=2.0)
+    kc, vc = rnd(g, B, 8, cap, 128), rnd(g, B, 8, cap, 128)
+    base = torch.tensor(bases, dtype=torch.int64)
+    anc = [_tree_masks(T, 300 + b) for b in range(B)] if mode == "tree" else None
+    anc_t = (torch.tensor([[a - (1 << 64) if a >= 1 << 63 else a for a in row] for row in anc])
+             if anc is not None else None)
+    out = ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), base.to(DEV),
+                              anc_t.to(DEV) if anc_t is not None else None)
+    sync()
+    for b, o in enumerate(_block_ref_rows(q, kc, vc, base, anc, T)):
+        assert_ulp(out[b].cpu(), o, 2, f"ragged row {b}", abs_floor=p_round_bound(vc))
+
+
 def test_kv_compact(ops):
     say("kv_compact")
     g = torch.Generator().manual_seed(700)
