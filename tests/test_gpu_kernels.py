@@ -461,6 +461,22 @@ def test_decode_attention(ops, B, cap, pos):
     assert_ulp(out.cpu(), o_ref, 2, "attention out", abs_floor=p_round_bound(vcache, qkv))
 
 
+# Ragged decode attention: seeded random batch (the VALU unit at B = 1, the MFMA kernel above),
+# cache size and position, so the split plan, the last partial key tile and the split that holds
+# the new key vary from case to case
+_RNG_DA = np.random.default_rng(777)
+RAGGED_DA = []
+for _i in range(10):
+    _B = 1 if _i % 3 == 0 else int(_RNG_DA.integers(2, 41))
+    _cap = int(_RNG_DA.integers(33, 5001))
+    RAGGED_DA.append((_B, _cap, int(_RNG_DA.integers(0, _cap))))
+
+
+@pytest.mark.parametrize("B,cap,pos", RAGGED_DA)
+def test_decode_attention_ragged(ops, B, cap, pos):
+    test_decode_attention(ops, B, cap, pos)
+
+
 @pytest.mark.parametrize("B", [1, 2])
 @pytest.mark.parametrize("pos", [300, -1])
 def test_decode_attention_position_outside_cache_writes_nothing(ops, B, pos):
