@@ -363,6 +363,37 @@ def test_lm_head_argmax(ops, B):
     assert int(pos.item()) == 1                                  # position advanced once
 
 
+# Ragged vocabularies (multiples of 4 from 256 up) at row counts across the LM head's kernels:
+# every kernel's last, partly filled vocabulary block
+_RNG_LM = np.random.default_rng(31337)
+RAGGED_LM = [(int(_RNG_LM.choice([1, 2, 5, 17, 33, 64, 100, 129, 200, 256])),
+              int(_RNG_LM.integers(64, 12001)) * 4) for _ in range(8)]
+
+
+@pytest.mark.parametrize("B,V", RAGGED_LM)
+def test_lm_head_argmax_ragged_vocab(ops, B, V):
+    say(f"lm_head_argmax ragged B={B} V={V}")
+    g = torch.Generator().manual_seed(B * 131 + V)
+    K = 2560
+    w = rnd(g, V, K, scale=0.02)
+    x = rnd(g, B, K)
+    nw = rnd(g, K, scale=0.1) + 1
+    logits = torch.empty((B, V), dtype=torch.float32, device=DEV)
+    tok = ops.lm_head_argmax(x.to(DEV), w.to(DEV), nw.to(DEV), 1e-6, logits=logits)
+    sync()
+    exact = R.rmsnorm(x, nw).double() @ w.double().T
+    lg = logits.cpu()
+    assert float((lg.double() - exact).abs().max()) <= 2e-2      # north-star logits bar
+    if B >= 3:
+        # from 3 rows on the normalised input is the standalone RMSNorm kernel's, whose rstd
+        # reduction may move single bf16 elements by one ulp (~1e-3 in a logit); against that
+        # input the logits carry only fp32 accumulation error
+        hk = ops.rmsnorm(x.to(DEV), nw.to(DEV), 1e-6).cpu()
+        own_exact = hk.double() @ w.double().T
+        assert float((lg.double() - own_exact).abs().max()) <= 1e-4
+    assert torch.equal(tok.cpu(), torch.argmax(lg.to(BF).float(), dim=-1))
+
+
 @pytest.mark.parametrize("B", [1, 8, 40, 72, 256])
 def test_lm_head_ties_pick_lowest_index(ops, B):
     say(f"lm_head ties B={B}")
