@@ -438,6 +438,55 @@ def decode_ref(qkv, qn, kn, cos, sin, kcache, vcache, pos):
     return o[:, :, 0], kc, vc
 
 
+# Ragged blocks of tokens per sequence (the prefill / tree path: 8-token row blocks with a
+# partial last one), per-row base positions: every token's q, K and V against the oracle, and no
+# cache slot outside the block written
+_RNG_QK = np.random.default_rng(99)
+RAGGED_QK = [(int(_RNG_QK.integers(1, 5)), int(_RNG_QK.integers(1, 71))) for _ in range(6)]
+
+
+@pytest.mark.parametrize("B,T", RAGGED_QK)
+def test_qk_norm_rope_ragged_blocks(ops, B, T):
+    Hq, Hkv, cap = 32, 8, 700
+    say(f"qk_norm_rope ragged B={B} T={T} (per-row bases)")
+    g = torch.Generator().manual_seed(900 + 7 * B + T)
+    qkv = rnd(g, B * T, (Hq + 2 * Hkv) * 128, scale=2.0)
+    qn, kn = rnd(g, 128, scale=0.2) + 1, rnd(g, 128, scale=0.2) + 1
+    base = torch.randint(0, cap - T + 1, (B,), generator=g)
+    cos, sin = R.rope_tables(cap)
+    kc = torch.zeros((B, Hkv, cap, 128), dtype=BF, device=DEV)
+    vc = torch.zeros_like(kc)
+    q_out = torch.empty((B, T, Hq, 128), dtype=BF, device=DEV)
+    ops.qk_norm_rope(qkv.to(DEV), qn.to(DEV), kn.to(DEV), cos.to(DEV), sin.to(DEV), base.to(DEV),
+                     ops.POS_ROW, q_out, kc, vc, B, T, Hq, Hkv, 1e-6)
+    sync()
+    x = qkv.view(B, T, Hq + 2 * Hkv, 128)
+    slots = base[:, None] + torch.arange(T)[None]                       # [B, T]
+    c, sn = cos[slots][:, :, None, :], sin[slots][:, :, None, :]
+    q_ref, k_ref = R.qk_norm_rope(x[:, :, :Hq], x[:, :, Hq:Hq + Hkv], qn, kn, cos[slots], sin[slots])
+
+    def check(got, ref, h, nw, what):
+        # the head's rstd may differ from the oracle's by its reduction order, moving a normalised
+        # value by one ulp; where the rotation's two products cancel, that ulp of each product
+        # survives into a small output: bound = 2 ulp(out) + ulp(y c) + ulp(rot(y) s)
+        y = R.rmsnorm(h, nw).float()
+        bound = (2 * bf16_ulp(torch.maximum(got.float().abs(), ref.float().abs()))
+                 + bf16_ulp((y * c.float()).abs()) + bf16_ulp((R.rotate_half(y) * sn.float()).abs()))
+        d = (got.float() - ref.float()).abs()
+        assert bool((d <= bound).all()), f"{what}: max excess {float((d - bound).max())}"
+
+    check(q_out.cpu(), q_ref, x[:, :, :Hq], qn, "q")
+    kcc, vcc = kc.cpu(), vc.cpu()
+    check(kcc.permute(0, 2, 1, 3).gather(1, slots[:, :, None, None].expand(B, T, Hkv, 128)), k_ref,
+          x[:, :, Hq:Hq + Hkv], kn, "k cache")
+    for b in range(B):
+        sl = slice(int(base[b]), int(base[b]) + T)
+        assert torch.equal(vcc[b, :, sl].transpose(0, 1), x[b, :, Hq + Hkv:])
+        kcc[b, :, sl] = 0
+        vcc[b, :, sl] = 0
+    assert not bool(kcc.any()) and not bool(vcc.any())                 # nothing else written
+
+
 @pytest.mark.parametrize("B", [1, 4])
 def test_qk_norm_rope_matches_decode_unit_bitwise(ops, B):
     """The standalone q/k norm + RoPE kernel (prefill chunks, tree verification: 16 lanes per
